@@ -1,0 +1,218 @@
+"""Throughput of the MI355X flash_attention_v2 on the BASELINE.json configs.
+
+Default: config c2 (dense causal GQA, B2 Hq32 Hkv8 L2048 D128, bf16), the
+configuration BASELINE.json's metric is quoted on.  A "step" is one
+``flash_attention_v2`` call over the whole batch with inputs already
+resident in HBM.  Prints ONE JSON line (rank 0, N=1):
+
+  value       algorithmic TFLOP/s of the whole step (host wall clock over K
+              steps, bracketed by torch.cuda.synchronize());
+  roofline    achieved TFLOP/s of the forward kernel from HIP events recorded
+              around every step on the stream the kernels run on, against
+              the dense bf16/fp16 MFMA peak (256 CU x 4096 FLOP/clk x 2.4 GHz);
+  cpu_baseline  the reference test suite's oracle (fp32 SDPA per sequence,
+              oracle.sdpa_reference) on the host CPU, on a bounded sample.
+
+  python bench.py [--steps K] [--warmup W] [--config c2] [--dtype bf16]
+                  [--no-cpu] [--flush]
+
+``--gpus N`` with N > 1 exits: this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "triton-kernels_amd"))
+
+import workloads as W  # noqa: E402
+
+PEAK_TFLOPS = 256 * 4096 * 2.4e9 / 1e12  # 2516.6 dense bf16/fp16 MFMA
+PEAK_HBM_GBS = 8000.0
+METRIC = "TFLOP/s + % of bf16 MFMA peak, flash_attention_v2 causal GQA seq2048 d128"
+DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16, "f16": torch.float16,
+          "fp32": torch.float32, "f32": torch.float32}
+DTYPE_NAME = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
+DESCR = {
+    "c1": "c1 dense causal MHA B1 H8 L512 D64",
+    "c2": "c2 dense causal GQA B2 Hq32 Hkv8 L2048 D128",
+    "c3": "c3 ragged causal self 16 seqs L~U[128,4096] Hq32 Hkv8 D128",
+    "c4": "c4 paged chunked prefill 32 seqs ctx~U[512,8192] page16 q=last128 Hq32 Hkv8 D128",
+    "c5": "c5 non-causal MQA cross B4 Hq32 Hkv1 q1024 kv16384 D128",
+}
+
+
+def cpu_baseline(w: W.Workload, budget_s: float = 20.0):
+    """fp32 SDPA per sequence on host cores (oracle.sdpa_reference, i.e. the
+    reference suite's oracle, tests/test_attention.py:80-98), 1 warmup + 3
+    timed reps, median; sample = as many whole (sequence, kv-head group)
+    units as fit the budget."""
+    import oracle
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    qs, ks, vs = W.sequences(w)
+    g = w.q_heads // w.kv_heads
+    units = [(b, kh) for b in range(len(qs)) for kh in range(w.kv_heads)]
+
+    def unit_call(b, kh):
+        q = qs[b][:, kh * g:(kh + 1) * g]
+        k = ks[b][:, kh:kh + 1]
+        v = vs[b][:, kh:kh + 1]
+        if w.is_causal and w.causal_alignment == "bottom_right":
+            return oracle.sdpa_reference_bottom_right([q], [k], [v], g, 1)
+        return oracle.sdpa_reference([q], [k], [v], g, 1, w.is_causal)
+
+    def unit_flops(b):
+        return 4.0 * w.head_dim * g * W.visible_pairs(w.q_lens[b], w.kv_lens[b], w.is_causal,
+                                                       w.causal_alignment)
+
+    # time one unit to size the sample
+    t0 = time.perf_counter()
+    unit_call(*units[0])
+    one = max(time.perf_counter() - t0, 1e-4)
+    n = max(1, min(len(units), int(budget_s / 4 / one)))
+    step = max(1, len(units) // n)
+    sample = units[::step][:n]
+    fl = sum(unit_flops(b) for b, _ in sample)
+    for b, kh in sample[:1]:
+        unit_call(b, kh)  # warmup
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for b, kh in sample:
+            unit_call(b, kh)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    return {
+        "value": round(fl / med / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{len(sample)} of {len(units)} (sequence, kv-head group) units of "
+                  f"{w.name}, fp32 SDPA per sequence with repeat_interleaved KV heads, "
+                  f"{fl / 1e9:.1f} GFLOP per rep, median of 3",
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=W.CONFIGS)
+    ap.add_argument("--dtype", default=None, choices=sorted(DTYPES))
+    ap.add_argument("--alignment", default=None, choices=["top_left", "bottom_right"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--flush", action="store_true",
+                    help="write 512 MiB between steps (outside the events) to flush L2/MALL")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the flash_attention_v2 hot path has no "
+              "multi-GPU component in this build (see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        return 2
+
+    from kernels import _fa2
+    from kernels.attention import flash_attention_v2
+
+    _fa2.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dt = DTYPES[args.dtype] if args.dtype else None
+    w_cpu = W.make(args.config, dtype=dt, causal_alignment=args.alignment)
+    w = w_cpu.to(dev)
+    kw = w.kwargs()
+    fl = W.flops(w)
+    nbytes = W.hbm_bytes(w)
+    flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if args.flush else None
+
+    def step():
+        return flash_attention_v2(w.q, w.k, w.v, **kw)
+
+    print(f"bench: {DESCR[args.config]} {DTYPE_NAME[w.dtype]} warmup={args.warmup} "
+          f"steps={args.steps}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        if flush_buf is not None:
+            flush_buf.fill_(i & 0xFF)
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    kern_avg = sum(kern_ms) / len(kern_ms)
+    kern_med = sorted(kern_ms)[len(kern_ms) // 2]
+    ms_per_step = wall * 1e3 / args.steps
+    if flush_buf is not None:
+        ms_per_step = kern_avg  # wall clock includes the flush writes
+    value = fl / (ms_per_step * 1e-3) / 1e12
+    achieved = fl / (kern_avg * 1e-3) / 1e12
+    bound = "mfma" if fl / nbytes > (PEAK_TFLOPS * 1e12) / (PEAK_HBM_GBS * 1e9) else "hbm"
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_NAME[w.dtype],
+        "data": "synthetic (seeded randn, CPU generator, seed 0)",
+        "config": {
+            "workload": DESCR[args.config],
+            "layout": w.layout,
+            "causal": w.is_causal,
+            "causal_alignment": w.causal_alignment if w.is_causal else None,
+            "gflop_per_step": round(fl / 1e9, 3),
+            "algorithmic_mb_per_step": round(nbytes / 1e6, 2),
+            "l2_mall_flushed": bool(args.flush),
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": bound,
+            "achieved": round(achieved, 2),
+            "peak": round(PEAK_TFLOPS, 1),
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": None,
+            "kernel_ms_avg": round(kern_avg, 5),
+            "kernel_ms_median": round(kern_med, 5),
+            "hbm_gbs_algorithmic": round(nbytes / (kern_avg * 1e-3) / 1e9, 1),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(w_cpu, args.cpu_budget)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

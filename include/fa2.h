@@ -1,0 +1,153 @@
+/*
+ * fa2.h - C ABI of the MI355X (gfx950) flash_attention_v2 forward pass.
+ *
+ * This is the drop-in boundary behind the Python entry point
+ * `flash_attention_v2(q, k, v, *, is_causal, q_indptr, kv_indptr,
+ * k_block_table, v_block_table, kv_page_size)`.
+ *
+ * Reference interface replaced (harsh-vsingh/triton-kernels):
+ *   kernels/attention.py:749-927  host wrapper `flash_attention_v2`
+ *   kernels/attention.py:430-656  `_flash_attentionv2_partial_kernel`
+ *   kernels/attention.py:659-746  `_flash_attentionv2_merge_kernel`
+ * The reference binds its kernels through Triton's launcher; the Python
+ * wrapper of this library binds these entry points through ctypes.
+ *
+ * All pointers are device pointers except `params` itself.  Sizes and
+ * strides are in ELEMENTS of the tensor they describe; the last (head_dim)
+ * dimension of q, k, v and o must be contiguous.  No entry point allocates
+ * device memory: scratch space comes from the caller through
+ * `workspace` (size from fa2_fwd_workspace_size).  No entry point performs a
+ * host<->device synchronisation; fa2_fwd only enqueues work on `stream`.
+ */
+#ifndef FA2_H_
+#define FA2_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Layout of q/k/v/o, the reference's `TYPE` constexpr
+ * (kernels/attention.py:465-514; mode select at :766-767). */
+enum fa2_layout {
+  FA2_LAYOUT_DENSE = 0,  /* q,o [B,Hq,M,D]; k,v [B,Hkv,N,D]                    */
+  FA2_LAYOUT_RAGGED = 1, /* q,o [Tq,Hq,D]; k,v [Tkv,Hkv,D]; q_indptr/kv_indptr
+                            are exclusive prefix sums, int32 [B+1]             */
+  FA2_LAYOUT_PAGED = 2   /* q,o [B,Hq,M,D]; k,v caches [pages*page_size,Hkv,D];
+                            kv_indptr holds per-sequence KV LENGTHS int32 [B];
+                            k/v_block_table int32 [B, >=ceil(len/page_size)] */
+};
+
+/* Element type of q, k, v and o (all four share it, attention.py:762). */
+enum fa2_dtype {
+  FA2_DTYPE_F16 = 0,  /* fp16 MFMA, fp32 accumulation                          */
+  FA2_DTYPE_BF16 = 1, /* bf16 MFMA, fp32 accumulation                          */
+  FA2_DTYPE_F32 = 2   /* operands rounded to fp16 as the reference does
+                         (attention.py:547,572,594,607,614,633), fp32 output   */
+};
+
+/* Causal mask.  TOP_LEFT is the reference's `is_causal=True`
+ * (attention.py:566-569: key j visible to query i iff j <= i, per-sequence
+ * local indices), identical to SDPA `is_causal=True`.  BOTTOM_RIGHT (key j
+ * visible iff j <= i + Lk - Lq) has no counterpart in the reference; it is
+ * the chunked-prefill alignment and is reachable only through this ABI or
+ * the wrapper's keyword `causal_alignment="bottom_right"`. */
+enum fa2_mask {
+  FA2_MASK_NONE = 0,
+  FA2_MASK_CAUSAL_TOP_LEFT = 1,
+  FA2_MASK_CAUSAL_BOTTOM_RIGHT = 2
+};
+
+/* Return codes. */
+enum fa2_status {
+  FA2_OK = 0,
+  FA2_ERR_NULL_POINTER = 1,
+  FA2_ERR_BAD_LAYOUT = 2,
+  FA2_ERR_BAD_DTYPE = 3,
+  FA2_ERR_BAD_MASK = 4,
+  FA2_ERR_BAD_SHAPE = 5,       /* negative sizes, Hq % Hkv != 0, ...          */
+  FA2_ERR_HEAD_DIM = 6,        /* head_dim not in the supported set            */
+  FA2_ERR_ALIGNMENT = 7,       /* a row start is not 16-byte aligned           */
+  FA2_ERR_PAGED_ARGS = 8,      /* missing table / page size / lengths          */
+  FA2_ERR_RAGGED_ARGS = 9,     /* missing indptr                                */
+  FA2_ERR_WORKSPACE = 10,      /* workspace missing or smaller than required   */
+  FA2_ERR_SPLITS = 11,         /* num_splits out of range                       */
+  FA2_ERR_HIP = 12,            /* a HIP runtime call or a launch failed         */
+  FA2_ERR_TOO_LARGE = 13       /* a size exceeds the kernels' 32-bit counters  */
+};
+
+/* Supported head dims (the reference accepts any power of two via
+ * tl.arange; these are the instantiated tile shapes). */
+#define FA2_MAX_SPLITS 64
+
+typedef struct fa2_params {
+  int32_t layout;     /* enum fa2_layout */
+  int32_t dtype;      /* enum fa2_dtype  */
+  int32_t mask;       /* enum fa2_mask   */
+  int32_t num_splits; /* split-KV factor: 0 = automatic, 1..FA2_MAX_SPLITS */
+
+  int64_t batch;      /* B (ragged: q_indptr.numel()-1)                       */
+  int64_t q_heads;    /* Hq                                                    */
+  int64_t kv_heads;   /* Hkv, Hq % Hkv == 0; q head h reads kv head h*Hkv/Hq  */
+  int64_t head_dim;   /* D                                                     */
+  int64_t q_len;      /* dense/paged: M (rows per sequence); ragged: Tq       */
+  int64_t kv_len;     /* dense: N; ragged: Tkv; paged: unused (lengths come
+                         from kv_indptr)                                       */
+
+  /* Element strides.  Dense/paged q and o use (batch, head, row); ragged q/o
+   * and every token-major k/v use (token, head) and ignore *_sb. */
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+
+  const int32_t* q_indptr;      /* ragged only                               */
+  const int32_t* kv_indptr;     /* ragged: prefix sums; paged: lengths       */
+  const int32_t* k_block_table; /* paged only                                */
+  const int32_t* v_block_table; /* paged only                                */
+  int64_t k_table_stride;       /* row stride of k_block_table (elements)    */
+  int64_t v_table_stride;       /* row stride of v_block_table (elements)    */
+  int64_t page_size;            /* tokens per page (paged only)              */
+
+  float softmax_scale;          /* reference: head_dim ** -0.5 (:897)        */
+  int32_t reserved0;
+
+  void* workspace;              /* device scratch, >= fa2_fwd_workspace_size */
+  size_t workspace_bytes;
+} fa2_params;
+
+/* Bytes of device workspace fa2_fwd needs for `p` (0 is possible).
+ * Replaces the reference's per-call torch.empty of running_sum/max/acc
+ * (attention.py:852-864).  Host-only: touches no device state except a
+ * one-time, cached query of the current device's compute-unit count. */
+int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes);
+
+/* Validate `p` and enqueue the forward pass on `stream` (a hipStream_t;
+ * NULL = the legacy default stream).  Replaces attention.py:836-925
+ * (split heuristic, workspace, partial + merge launches).  Returns FA2_OK
+ * or an error code; validation errors are reported before any launch. */
+int fa2_fwd(const fa2_params* p, void* stream);
+
+/* Static, human-readable text for a status code. */
+const char* fa2_strerror(int status);
+
+/* Version of this ABI (bumped on any change to fa2_params).  No counterpart
+ * in the reference: lets a binding refuse a library it was not written for. */
+int fa2_abi_version(void);
+
+/* sizeof(fa2_params) as compiled into the library.  No counterpart in the
+ * reference: lets an FFI binding (ctypes here) check its struct mirror. */
+size_t fa2_params_size(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA2_H_ */

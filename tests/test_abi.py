@@ -1,0 +1,139 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol
+include/fa2.h declares, its struct layout matches the ctypes mirror, and
+every validation error is reported before any device work."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from kernels import _fa2
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fa2.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(fa2_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_fa2.LIB_PATH)
+    names = declared_functions()
+    assert set(names) == set(_fa2.EXPORTS), names
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_struct_layout_matches():
+    assert _fa2.lib().fa2_params_size() == ctypes.sizeof(_fa2.Fa2Params)
+    assert _fa2.lib().fa2_abi_version() == 1
+
+
+def test_strerror_for_every_code():
+    seen = set()
+    for code in range(14):
+        msg = _fa2.lib().fa2_strerror(code).decode()
+        assert msg and "unknown" not in msg
+        seen.add(msg)
+    assert len(seen) == 14
+    assert "unknown" in _fa2.lib().fa2_strerror(999).decode()
+
+
+def dense_params(**kw):
+    p = _fa2.Fa2Params()
+    p.layout, p.dtype, p.mask, p.num_splits = 0, 1, 1, 1
+    p.batch, p.q_heads, p.kv_heads, p.head_dim, p.q_len, p.kv_len = 2, 8, 2, 128, 300, 300
+    p.q_sb, p.q_sh, p.q_ss = 8 * 300 * 128, 300 * 128, 128
+    p.k_sb, p.k_sh, p.k_ss = 2 * 300 * 128, 300 * 128, 128
+    p.v_sb, p.v_sh, p.v_ss = p.k_sb, p.k_sh, p.k_ss
+    p.o_sb, p.o_sh, p.o_ss = p.q_sb, p.q_sh, p.q_ss
+    p.softmax_scale = 128 ** -0.5
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def rc_ws(p):
+    n = ctypes.c_size_t(0)
+    return _fa2.lib().fa2_fwd_workspace_size(ctypes.byref(p), ctypes.byref(n)), n.value
+
+
+def rc_fwd(p):
+    return _fa2.lib().fa2_fwd(ctypes.byref(p), None)
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("layout", 3, 2), ("dtype", 7, 3), ("mask", 5, 4), ("q_heads", 7, 5), ("batch", -1, 5),
+    ("head_dim", 96, 6), ("q_ss", 100, 7), ("num_splits", 65, 11), ("num_splits", -1, 11),
+])
+def test_validation_errors(field, value, code):
+    p = dense_params(**{field: value})
+    assert rc_ws(p)[0] == code
+    assert rc_fwd(p) == code  # reported before any HIP call
+
+
+def test_null_params():
+    assert _fa2.lib().fa2_fwd(None, None) == 1
+    n = ctypes.c_size_t(0)
+    assert _fa2.lib().fa2_fwd_workspace_size(None, ctypes.byref(n)) == 1
+
+
+def test_ragged_and_paged_argument_checks():
+    p = dense_params(layout=1)
+    assert rc_ws(p)[0] == 9  # ragged without indptr
+    p = dense_params(layout=2, kv_indptr=16, k_block_table=16, v_block_table=16, page_size=0)
+    assert rc_ws(p)[0] == 8
+    p = dense_params(layout=2, kv_indptr=16, k_block_table=16, page_size=16)
+    assert rc_ws(p)[0] == 8
+
+
+def test_null_tensor_pointers_rejected_before_launch():
+    p = dense_params()
+    assert rc_fwd(p) == 1  # q/k/v/o NULL
+
+
+def test_workspace_sizes():
+    # dense, no split: nothing
+    assert rc_ws(dense_params()) == (0, 0)
+    # dense split 4: (m,l) + O partials for grid_x = ceil(300/128) * 2 * 8 workgroups
+    rc, n = rc_ws(dense_params(num_splits=4))
+    grid = 3 * 2 * 8
+    assert rc == 0 and n >= 4 * grid * 128 * (2 + 128) * 4
+    # ragged: work list of ceil(Tq/128) + B entries of 8 bytes + counter
+    p = dense_params(layout=1, q_indptr=16, kv_indptr=16, batch=5, q_len=1000, kv_len=1000)
+    rc, n = rc_ws(p)
+    assert rc == 0 and n >= (8 + 5) * 8 + 4
+    # empty problem: no workspace
+    assert rc_ws(dense_params(batch=0)) == (0, 0)
+
+
+def test_workspace_too_small_is_rejected():
+    p = dense_params(num_splits=2, q=16, k=16, v=16, o=16)
+    rc, n = rc_ws(p)
+    assert rc == 0 and n > 0
+    p.workspace, p.workspace_bytes = 16, n - 1
+    assert rc_fwd(p) == 10
+
+
+def test_wrapper_asserts_is_cuda_on_cpu_tensors():
+    from kernels.attention import flash_attention_v2
+    q = torch.zeros((1, 2, 8, 64), dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        flash_attention_v2(q, q, q)
+    with pytest.raises(AssertionError):
+        flash_attention_v2(q, q.to(torch.bfloat16), q)
+
+
+def test_product_path_does_not_import_the_oracle():
+    pkg = os.path.join(ROOT, "triton-kernels_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "from oracle" not in text, f
+                assert "fa2_oracle" not in text, f

@@ -1,0 +1,49 @@
+"""Build ``kernels/libfa2.so`` in-tree with hipcc for gfx950.
+
+Usage: ``python triton-kernels_amd/build.py`` (or ``build()`` from Python).
+The library is a plain C ABI (include/fa2.h); no torch extension machinery.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+SOURCES = [os.path.join(HERE, "csrc", "fa2_fwd.hip")]
+DEPS = SOURCES + [os.path.join(HERE, "csrc", "fa2_device.h"), os.path.join(ROOT, "include", "fa2.h")]
+OUT = os.path.join(HERE, "kernels", "libfa2.so")
+
+FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-I" + os.path.join(ROOT, "include"),
+    # packed fp32 VALU ops are kept out of all device code
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def build(verbose: bool = False) -> str:
+    tmp = OUT + ".tmp"
+    cmd = [HIPCC] + FLAGS + SOURCES + ["-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,260 @@
+// fa2_fwd.hip - C ABI and launch logic of the gfx950 flash_attention_v2
+// forward pass (declared in include/fa2.h).
+//
+// Replaces the host half of harsh-vsingh/triton-kernels
+// kernels/attention.py:836-925: split heuristic (:836-841), workspace
+// (:852-864) and the partial + merge launches (:882-925).  Differences:
+//   * when the grid already fills the GPU no split is made and the forward
+//     kernel writes O directly (the reference always writes fp32 partials and
+//     launches a merge, even for split_k == 1);
+//   * ragged/paged schedules come from a device-side plan kernel, so there is
+//     no `.item()` host synchronisation (attention.py:847);
+//   * no allocation: the caller passes the workspace.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+#include "fa2_device.h"
+
+namespace fa2 {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_cu_once[kMaxDevices];
+int g_cu_count[kMaxDevices];
+
+int cu_count_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::call_once(g_cu_once[dev], [dev] {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_cu_count[dev] = n;
+  });
+  return g_cu_count[dev];
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int elt_bytes(int dtype) { return dtype == FA2_DTYPE_F32 ? 4 : 2; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool stride_ok(int64_t s, int eb) { return ((s * eb) & 15) == 0; }
+
+// Number of work units (q-block x head) the forward launch covers, and the
+// capacity of the ragged/paged work list.
+struct Plan {
+  int64_t work_ub;  // (sequence, q-block) slots
+  int64_t grid_x;   // work_ub * Hq
+  int splits;
+  size_t off_work, off_count, off_ml, off_o, total;
+};
+
+int validate(const fa2_params* p) {
+  if (!p) return FA2_ERR_NULL_POINTER;
+  if (p->layout < FA2_LAYOUT_DENSE || p->layout > FA2_LAYOUT_PAGED) return FA2_ERR_BAD_LAYOUT;
+  if (p->dtype < FA2_DTYPE_F16 || p->dtype > FA2_DTYPE_F32) return FA2_ERR_BAD_DTYPE;
+  if (p->mask < FA2_MASK_NONE || p->mask > FA2_MASK_CAUSAL_BOTTOM_RIGHT) return FA2_ERR_BAD_MASK;
+  if (p->head_dim != 64 && p->head_dim != 128) return FA2_ERR_HEAD_DIM;
+  if (p->batch < 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->q_len < 0 || p->kv_len < 0)
+    return FA2_ERR_BAD_SHAPE;
+  if (p->q_heads % p->kv_heads != 0) return FA2_ERR_BAD_SHAPE;
+  if (p->num_splits < 0 || p->num_splits > FA2_MAX_SPLITS) return FA2_ERR_SPLITS;
+  if (p->layout == FA2_LAYOUT_RAGGED && (!p->q_indptr || !p->kv_indptr)) return FA2_ERR_RAGGED_ARGS;
+  if (p->layout == FA2_LAYOUT_PAGED &&
+      (!p->kv_indptr || !p->k_block_table || !p->v_block_table || p->page_size <= 0 ||
+       p->k_table_stride < 0 || p->v_table_stride < 0))
+    return FA2_ERR_PAGED_ARGS;
+  const int eb = elt_bytes(p->dtype);
+  const int64_t strides[] = {p->q_sb, p->q_sh, p->q_ss, p->k_sb, p->k_sh, p->k_ss,
+                             p->v_sb, p->v_sh, p->v_ss, p->o_sb, p->o_sh, p->o_ss};
+  for (int64_t s : strides)
+    if (!stride_ok(s, eb)) return FA2_ERR_ALIGNMENT;
+  // 32-bit counters inside the kernels
+  const int64_t lim = INT32_MAX / 2;
+  if (p->batch > lim || p->q_heads > 65536 || p->q_len > lim || p->kv_len > lim ||
+      p->page_size > lim)
+    return FA2_ERR_TOO_LARGE;
+  return FA2_OK;
+}
+
+bool empty_problem(const fa2_params* p) {
+  return p->batch == 0 || p->q_len == 0;
+}
+
+int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
+  const int64_t nqb = cdiv(p->q_len, kBM);
+  if (p->layout == FA2_LAYOUT_DENSE)
+    pl->work_ub = nqb * p->batch;
+  else if (p->layout == FA2_LAYOUT_RAGGED)
+    pl->work_ub = nqb + p->batch;  // sum_b ceil(Lq_b/BM) <= ceil(Tq/BM) + B
+  else
+    pl->work_ub = nqb * p->batch;
+  pl->grid_x = pl->work_ub * p->q_heads;
+  if (pl->grid_x > INT32_MAX || pl->work_ub > INT32_MAX) return FA2_ERR_TOO_LARGE;
+
+  int splits = p->num_splits;
+  if (splits == 0) {
+    // Split the KV sweep only when the grid cannot fill the GPU (two
+    // resident workgroups per CU) and every split keeps >= 4 KV tiles.
+    const int64_t cus = query_device ? cu_count_current_device() : 256;
+    const int64_t slots = 2 * cus;
+    int64_t kv_ub = p->kv_len;
+    if (p->layout == FA2_LAYOUT_PAGED) kv_ub = INT32_MAX;  // lengths live on the device
+    const int64_t tiles = cdiv(kv_ub, kBN);
+    splits = 1;
+    if (pl->grid_x > 0 && pl->grid_x < slots) {
+      int64_t s = cdiv(slots, pl->grid_x);
+      const int64_t by_tiles = tiles / 4;
+      if (s > by_tiles) s = by_tiles;
+      if (s > FA2_MAX_SPLITS) s = FA2_MAX_SPLITS;
+      if (s < 1) s = 1;
+      splits = static_cast<int>(s);
+    }
+  }
+  pl->splits = splits;
+
+  size_t off = 0;
+  pl->off_work = off;
+  if (p->layout != FA2_LAYOUT_DENSE) off += static_cast<size_t>(pl->work_ub) * sizeof(int2);
+  off = (off + 255) & ~size_t(255);
+  pl->off_count = off;
+  if (p->layout != FA2_LAYOUT_DENSE) off += 256;
+  pl->off_ml = off;
+  if (splits > 1) off += static_cast<size_t>(splits) * pl->grid_x * kBM * 2 * sizeof(float);
+  off = (off + 255) & ~size_t(255);
+  pl->off_o = off;
+  if (splits > 1)
+    off += static_cast<size_t>(splits) * pl->grid_x * kBM * p->head_dim * sizeof(float);
+  pl->total = off;
+  return FA2_OK;
+}
+
+template <int DT, int D, int MODE>
+int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
+  if constexpr (MODE != FA2_LAYOUT_DENSE) {
+    hipLaunchKernelGGL((fa2_plan_kernel<MODE>), dim3(1), dim3(kPlanThreads), 0, st, a,
+                       const_cast<int2*>(a.work), const_cast<int32_t*>(a.work_count));
+  }
+  hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE>), dim3(pl.grid_x, pl.splits), dim3(kThreads), 0,
+                     st, a);
+  if (pl.splits > 1) {
+    hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), dim3(pl.grid_x), dim3(kThreads), 0, st,
+                       a);
+  }
+  return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
+}
+
+template <int DT, int D>
+int launch_mode(int mode, const KArgs& a, const Plan& pl, hipStream_t st) {
+  switch (mode) {
+    case FA2_LAYOUT_DENSE: return launch_typed<DT, D, FA2_LAYOUT_DENSE>(a, pl, st);
+    case FA2_LAYOUT_RAGGED: return launch_typed<DT, D, FA2_LAYOUT_RAGGED>(a, pl, st);
+    default: return launch_typed<DT, D, FA2_LAYOUT_PAGED>(a, pl, st);
+  }
+}
+
+template <int DT>
+int launch_dim(int d, int mode, const KArgs& a, const Plan& pl, hipStream_t st) {
+  if (d == 64) return launch_mode<DT, 64>(mode, a, pl, st);
+  return launch_mode<DT, 128>(mode, a, pl, st);
+}
+
+}  // namespace
+}  // namespace fa2
+
+using namespace fa2;
+
+extern "C" int fa2_abi_version(void) { return 1; }
+
+extern "C" size_t fa2_params_size(void) { return sizeof(fa2_params); }
+
+extern "C" const char* fa2_strerror(int s) {
+  switch (s) {
+    case FA2_OK: return "success";
+    case FA2_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case FA2_ERR_BAD_LAYOUT: return "layout must be dense (0), ragged (1) or paged (2)";
+    case FA2_ERR_BAD_DTYPE: return "dtype must be f16 (0), bf16 (1) or f32 (2)";
+    case FA2_ERR_BAD_MASK: return "mask must be none (0), top-left causal (1) or bottom-right causal (2)";
+    case FA2_ERR_BAD_SHAPE: return "invalid shape (negative size or q_heads % kv_heads != 0)";
+    case FA2_ERR_HEAD_DIM: return "unsupported head_dim (supported: 64, 128)";
+    case FA2_ERR_ALIGNMENT: return "tensor rows must start on 16-byte boundaries";
+    case FA2_ERR_PAGED_ARGS: return "paged layout needs kv_indptr (lengths), both block tables and page_size > 0";
+    case FA2_ERR_RAGGED_ARGS: return "ragged layout needs q_indptr and kv_indptr";
+    case FA2_ERR_WORKSPACE: return "workspace is missing or smaller than fa2_fwd_workspace_size";
+    case FA2_ERR_SPLITS: return "num_splits must be in [0, FA2_MAX_SPLITS]";
+    case FA2_ERR_HIP: return "a HIP launch or runtime call failed";
+    case FA2_ERR_TOO_LARGE: return "a size exceeds the kernels' 32-bit index range";
+    default: return "unknown fa2 status";
+  }
+}
+
+extern "C" int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes) {
+  if (!bytes) return FA2_ERR_NULL_POINTER;
+  int s = validate(p);
+  if (s != FA2_OK) return s;
+  if (empty_problem(p)) {
+    *bytes = 0;
+    return FA2_OK;
+  }
+  Plan pl;
+  s = make_plan(p, &pl, p->num_splits == 0);
+  if (s != FA2_OK) return s;
+  *bytes = pl.total;
+  return FA2_OK;
+}
+
+extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
+  int s = validate(p);
+  if (s != FA2_OK) return s;
+  if (empty_problem(p)) return FA2_OK;
+  if (!p->q || !p->k || !p->v || !p->o) return FA2_ERR_NULL_POINTER;
+  if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o))
+    return FA2_ERR_ALIGNMENT;
+  Plan pl;
+  s = make_plan(p, &pl, p->num_splits == 0);
+  if (s != FA2_OK) return s;
+  if (pl.total > 0 && (!p->workspace || p->workspace_bytes < pl.total)) return FA2_ERR_WORKSPACE;
+
+  KArgs a{};
+  a.q = p->q;
+  a.k = p->k;
+  a.v = p->v;
+  a.o = p->o;
+  a.q_indptr = p->q_indptr;
+  a.kv_indptr = p->kv_indptr;
+  a.k_table = p->k_block_table;
+  a.v_table = p->v_block_table;
+  a.q_sb = p->q_sb; a.q_sh = p->q_sh; a.q_ss = p->q_ss;
+  a.k_sb = p->k_sb; a.k_sh = p->k_sh; a.k_ss = p->k_ss;
+  a.v_sb = p->v_sb; a.v_sh = p->v_sh; a.v_ss = p->v_ss;
+  a.o_sb = p->o_sb; a.o_sh = p->o_sh; a.o_ss = p->o_ss;
+  a.k_table_stride = p->k_table_stride;
+  a.v_table_stride = p->v_table_stride;
+  a.batch = static_cast<int32_t>(p->batch);
+  a.hq = static_cast<int32_t>(p->q_heads);
+  a.hkv = static_cast<int32_t>(p->kv_heads);
+  a.q_len = static_cast<int32_t>(p->q_len);
+  a.kv_len = static_cast<int32_t>(p->kv_len);
+  a.page_size = static_cast<int32_t>(p->page_size > 0 ? p->page_size : 1);
+  a.nqb = static_cast<int32_t>(cdiv(p->q_len, kBM));
+  a.work_ub = static_cast<int32_t>(pl.work_ub);
+  a.mask = p->mask;
+  a.num_splits = pl.splits;
+  a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+  char* ws = static_cast<char*>(p->workspace);
+  a.work = p->layout != FA2_LAYOUT_DENSE ? reinterpret_cast<const int2*>(ws + pl.off_work) : nullptr;
+  a.work_count =
+      p->layout != FA2_LAYOUT_DENSE ? reinterpret_cast<const int32_t*>(ws + pl.off_count) : nullptr;
+  a.part_ml = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
+  a.part_o = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (p->dtype) {
+    case FA2_DTYPE_F16: return launch_dim<FA2_DTYPE_F16>(p->head_dim, p->layout, a, pl, st);
+    case FA2_DTYPE_BF16: return launch_dim<FA2_DTYPE_BF16>(p->head_dim, p->layout, a, pl, st);
+    default: return launch_dim<FA2_DTYPE_F32>(p->head_dim, p->layout, a, pl, st);
+  }
+}

@@ -1,0 +1,114 @@
+"""ctypes binding of ``libfa2.so`` (the C ABI declared in include/fa2.h).
+
+The library is built in-tree by ``triton-kernels_amd/build.py`` (hipcc,
+``--offload-arch=gfx950``).  There is no fallback: if the library is missing
+or does not load, every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfa2.so")
+
+LAYOUT_DENSE, LAYOUT_RAGGED, LAYOUT_PAGED = 0, 1, 2
+DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
+MASK_NONE, MASK_TOP_LEFT, MASK_BOTTOM_RIGHT = 0, 1, 2
+MAX_SPLITS = 64
+
+# Every symbol include/fa2.h declares.
+EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_strerror", "fa2_abi_version",
+           "fa2_params_size")
+
+
+class Fa2Params(ctypes.Structure):
+    """Mirror of ``struct fa2_params`` (include/fa2.h)."""
+
+    _fields_ = [
+        ("layout", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("mask", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("q_heads", ctypes.c_int64),
+        ("kv_heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("q_len", ctypes.c_int64),
+        ("kv_len", ctypes.c_int64),
+        ("q_sb", ctypes.c_int64), ("q_sh", ctypes.c_int64), ("q_ss", ctypes.c_int64),
+        ("k_sb", ctypes.c_int64), ("k_sh", ctypes.c_int64), ("k_ss", ctypes.c_int64),
+        ("v_sb", ctypes.c_int64), ("v_sh", ctypes.c_int64), ("v_ss", ctypes.c_int64),
+        ("o_sb", ctypes.c_int64), ("o_sh", ctypes.c_int64), ("o_ss", ctypes.c_int64),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("q_indptr", ctypes.c_void_p),
+        ("kv_indptr", ctypes.c_void_p),
+        ("k_block_table", ctypes.c_void_p),
+        ("v_block_table", ctypes.c_void_p),
+        ("k_table_stride", ctypes.c_int64),
+        ("v_table_stride", ctypes.c_int64),
+        ("page_size", ctypes.c_int64),
+        ("softmax_scale", ctypes.c_float),
+        ("reserved0", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib():
+    """Load libfa2.so once; raise a clear error when it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"flash_attention_v2: HIP library not built ({LIB_PATH} missing); "
+                    "run `python triton-kernels_amd/build.py` (hipcc, gfx950)")
+            L = ctypes.CDLL(LIB_PATH)
+            L.fa2_fwd_workspace_size.argtypes = [ctypes.POINTER(Fa2Params),
+                                                 ctypes.POINTER(ctypes.c_size_t)]
+            L.fa2_fwd_workspace_size.restype = ctypes.c_int
+            L.fa2_fwd.argtypes = [ctypes.POINTER(Fa2Params), ctypes.c_void_p]
+            L.fa2_fwd.restype = ctypes.c_int
+            L.fa2_strerror.argtypes = [ctypes.c_int]
+            L.fa2_strerror.restype = ctypes.c_char_p
+            L.fa2_abi_version.argtypes = []
+            L.fa2_abi_version.restype = ctypes.c_int
+            L.fa2_params_size.argtypes = []
+            L.fa2_params_size.restype = ctypes.c_size_t
+            if L.fa2_params_size() != ctypes.sizeof(Fa2Params):
+                raise RuntimeError("libfa2.so: fa2_params layout mismatch with the binding")
+            _lib = L
+    return _lib
+
+
+class Fa2Error(RuntimeError):
+    def __init__(self, code: int):
+        msg = lib().fa2_strerror(code).decode()
+        super().__init__(f"flash_attention_v2: {msg} (fa2 status {code})")
+        self.code = code
+
+
+def workspace_size(p: Fa2Params) -> int:
+    n = ctypes.c_size_t(0)
+    rc = lib().fa2_fwd_workspace_size(ctypes.byref(p), ctypes.byref(n))
+    if rc != 0:
+        raise Fa2Error(rc)
+    return n.value
+
+
+def forward(p: Fa2Params, stream: int) -> None:
+    rc = lib().fa2_fwd(ctypes.byref(p), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise Fa2Error(rc)

@@ -1,0 +1,284 @@
+"""Seeded inputs and work accounting for the five BASELINE.json configs.
+
+Shared by bench.py, tests/ and __graft_entry__.  Inputs are generated on the
+CPU with ``torch.Generator().manual_seed(seed)`` (values ``randn`` in fp32,
+then cast), so the same bits reach every device.  Packing helpers build the
+three layouts of ``flash_attention_v2`` from per-sequence ``[L,H,D]``
+tensors the way the reference test suite does (tests/test_attention.py:
+159-243), plus the shuffled-pool / ``-1``-padded paged cache of the
+reference benchmark (benchmarks/attention.py:351-431) with independent K and
+V page permutations.
+
+c1  dense causal MHA      1x8x512x64 fp16
+c2  dense causal GQA      B2 Hq32 Hkv8 L2048 D128 (fp16, bf16)
+c3  ragged causal self    16 seqs, L ~ U[128,4096], Hq32 Hkv8 D128 bf16
+c4  paged chunked prefill 32 seqs, ctx ~ U[512,8192], page 16, shuffled pool
+                          of ceil(sum/16)+256 pages, q = last 128 tokens
+                          (bottom-right causal), Hq32 Hkv8 D128 bf16
+c5  non-causal MQA cross  B4 Hq32 Hkv1 q1024 kv16384 D128 bf16 (+fp32 run)
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+CONFIGS = ("c1", "c2", "c3", "c4", "c5")
+PAGE = 16
+
+
+@dataclass
+class Workload:
+    name: str
+    layout: str                 # dense | ragged | paged
+    dtype: torch.dtype
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    is_causal: bool
+    causal_alignment: str = "top_left"
+    q_indptr: torch.Tensor | None = None
+    kv_indptr: torch.Tensor | None = None
+    k_block_table: torch.Tensor | None = None
+    v_block_table: torch.Tensor | None = None
+    kv_page_size: int | None = None
+    q_lens: list = field(default_factory=list)
+    kv_lens: list = field(default_factory=list)
+    q_heads: int = 0
+    kv_heads: int = 0
+    head_dim: int = 0
+
+    def kwargs(self) -> dict:
+        kw = dict(is_causal=self.is_causal)
+        if self.causal_alignment != "top_left":
+            kw["causal_alignment"] = self.causal_alignment
+        for n in ("q_indptr", "kv_indptr", "k_block_table", "v_block_table", "kv_page_size"):
+            val = getattr(self, n)
+            if val is not None:
+                kw[n] = val
+        return kw
+
+    def to(self, device) -> "Workload":
+        out = Workload(**{f: getattr(self, f) for f in self.__dataclass_fields__})
+        for n in ("q", "k", "v", "q_indptr", "kv_indptr", "k_block_table", "v_block_table"):
+            t = getattr(out, n)
+            if t is not None:
+                setattr(out, n, t.to(device))
+        return out
+
+
+# ---------------------------------------------------------------------------
+# algorithmic work
+# ---------------------------------------------------------------------------
+
+def visible_pairs(Lq: int, Lk: int, is_causal: bool, alignment: str = "top_left") -> int:
+    """Number of (query, key) pairs the mask admits."""
+    if not is_causal:
+        return Lq * Lk
+    off = (Lk - Lq) if alignment == "bottom_right" else 0
+    total = 0
+    # rows i with i + off + 1 keys, clipped to [0, Lk]
+    for i in range(Lq):
+        total += min(max(i + off + 1, 0), Lk)
+    return total
+
+
+def flops(w: Workload) -> float:
+    """4 * D * Hq * sum of visible pairs (QK^T and PV, 2 FLOP per MAC)."""
+    pairs = sum(visible_pairs(lq, lk, w.is_causal, w.causal_alignment)
+                for lq, lk in zip(w.q_lens, w.kv_lens))
+    return 4.0 * w.head_dim * w.q_heads * pairs
+
+
+def hbm_bytes(w: Workload) -> float:
+    """Q and O once at Hq, K and V once at Hkv (tokens actually attended)."""
+    es = torch.tensor([], dtype=w.dtype).element_size()
+    sq = sum(w.q_lens) if w.layout == "ragged" else w.q.shape[0] * w.q.shape[2]
+    sk = sum(w.kv_lens)
+    return es * w.head_dim * (2 * sq * w.q_heads + 2 * sk * w.kv_heads)
+
+
+# ---------------------------------------------------------------------------
+# packing (per-sequence [L,H,D] -> layouts)
+# ---------------------------------------------------------------------------
+
+def pack_dense(seqs, L: int) -> torch.Tensor:
+    """[L_b,H,D] list -> zero-padded [B,H,L,D] (tests/test_attention.py:159-170)."""
+    B, H, D = len(seqs), seqs[0].shape[1], seqs[0].shape[2]
+    out = torch.zeros((B, H, L, D), dtype=seqs[0].dtype, device=seqs[0].device)
+    for b, s in enumerate(seqs):
+        out[b, :, : s.shape[0]] = s.transpose(0, 1)
+    return out
+
+
+def indptr(lens, device="cpu") -> torch.Tensor:
+    return torch.tensor([0] + list(lens), dtype=torch.int32, device=device).cumsum(0).to(torch.int32)
+
+
+def paged_cache_contiguous(seqs, page: int):
+    """Reference test construction (tests/test_attention.py:101-134): pages in
+    sequence order, tail slots zero, unused table entries 0."""
+    lens = [s.shape[0] for s in seqs]
+    H, D = seqs[0].shape[1], seqs[0].shape[2]
+    nb = [(n + page - 1) // page for n in lens]
+    cache = torch.zeros((sum(nb) * page, H, D), dtype=seqs[0].dtype)
+    table = torch.zeros((len(seqs), max(nb) if nb else 0), dtype=torch.int32)
+    cur = 0
+    for b, s in enumerate(seqs):
+        for j in range(nb[b]):
+            table[b, j] = cur
+            chunk = s[j * page: min((j + 1) * page, lens[b])]
+            cache[cur * page: cur * page + chunk.shape[0]] = chunk
+            cur += 1
+    return cache, table
+
+
+def paged_cache_shuffled(seqs, page: int, extra_pages: int, gen: torch.Generator,
+                         fill: float | None = None):
+    """Pool of ceil(sum/page)+extra pages in a random order, table padded with
+    -1 (benchmarks/attention.py:415-420).  Unused pool slots hold ``fill``
+    (NaN by default, so a read outside the table shows up in the output)."""
+    lens = [s.shape[0] for s in seqs]
+    H, D = seqs[0].shape[1], seqs[0].shape[2]
+    nb = [(n + page - 1) // page for n in lens]
+    pool = sum(nb) + extra_pages
+    perm = torch.randperm(pool, generator=gen)
+    cache = torch.full((pool * page, H, D), float("nan") if fill is None else fill,
+                       dtype=seqs[0].dtype)
+    table = torch.full((len(seqs), max(nb) if nb else 0), -1, dtype=torch.int32)
+    cur = 0
+    for b, s in enumerate(seqs):
+        for j in range(nb[b]):
+            pg = int(perm[cur])
+            cur += 1
+            table[b, j] = pg
+            chunk = s[j * page: min((j + 1) * page, lens[b])]
+            cache[pg * page: pg * page + chunk.shape[0]] = chunk
+            if chunk.shape[0] < page:
+                cache[pg * page + chunk.shape[0]: (pg + 1) * page] = 0
+    return cache, table
+
+
+def gather_paged(cache, table, lens, page):
+    """Inverse of the paged construction: list of [L_b,H,D] sequences."""
+    out = []
+    for b, n in enumerate(lens):
+        rows = [int(table[b, j // page]) * page + j % page for j in range(n)]
+        out.append(cache[rows])
+    return out
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs
+# ---------------------------------------------------------------------------
+
+def _randn(gen, shape, dtype):
+    return torch.randn(shape, generator=gen, dtype=torch.float32).to(dtype)
+
+
+def make(name: str, dtype: torch.dtype | None = None, seed: int = 0,
+         causal_alignment: str | None = None) -> Workload:
+    """Build config ``name`` on the CPU.  ``dtype`` overrides the default."""
+    gen = torch.Generator().manual_seed(seed)
+    if name == "c1":
+        dt = dtype or torch.float16
+        B, H, L, D = 1, 8, 512, 64
+        q, k, v = (_randn(gen, (B, H, L, D), dt) for _ in range(3))
+        return Workload("c1", "dense", dt, q, k, v, True, q_lens=[L] * B, kv_lens=[L] * B,
+                        q_heads=H, kv_heads=H, head_dim=D)
+    if name == "c2":
+        dt = dtype or torch.bfloat16
+        B, Hq, Hkv, L, D = 2, 32, 8, 2048, 128
+        q = _randn(gen, (B, Hq, L, D), dt)
+        k = _randn(gen, (B, Hkv, L, D), dt)
+        v = _randn(gen, (B, Hkv, L, D), dt)
+        return Workload("c2", "dense", dt, q, k, v, True, q_lens=[L] * B, kv_lens=[L] * B,
+                        q_heads=Hq, kv_heads=Hkv, head_dim=D)
+    if name == "c3":
+        dt = dtype or torch.bfloat16
+        Hq, Hkv, D = 32, 8, 128
+        lens = torch.randint(128, 4097, (16,), generator=gen).tolist()
+        T = sum(lens)
+        q = _randn(gen, (T, Hq, D), dt)
+        k = _randn(gen, (T, Hkv, D), dt)
+        v = _randn(gen, (T, Hkv, D), dt)
+        ip = indptr(lens)
+        return Workload("c3", "ragged", dt, q, k, v, True, q_indptr=ip, kv_indptr=ip.clone(),
+                        q_lens=lens, kv_lens=lens, q_heads=Hq, kv_heads=Hkv, head_dim=D)
+    if name == "c4":
+        dt = dtype or torch.bfloat16
+        B, Hq, Hkv, D, QL = 32, 32, 8, 128, 128
+        ctx = torch.randint(512, 8193, (B,), generator=gen).tolist()
+        nb = [(c + PAGE - 1) // PAGE for c in ctx]
+        pool = sum(nb) + 256
+        width = max(nb)
+        # physical caches filled directly (every pool slot random), then two
+        # independent page permutations give the K and V tables
+        kc = _randn(gen, (pool * PAGE, Hkv, D), dt)
+        vc = _randn(gen, (pool * PAGE, Hkv, D), dt)
+        kperm = torch.randperm(pool, generator=gen)
+        vperm = torch.randperm(pool, generator=gen)
+        kt = torch.full((B, width), -1, dtype=torch.int32)
+        vt = torch.full((B, width), -1, dtype=torch.int32)
+        cur = 0
+        for b in range(B):
+            kt[b, : nb[b]] = kperm[cur: cur + nb[b]].to(torch.int32)
+            vt[b, : nb[b]] = vperm[cur: cur + nb[b]].to(torch.int32)
+            cur += nb[b]
+        q = _randn(gen, (B, Hq, QL, D), dt)
+        lens_t = torch.tensor(ctx, dtype=torch.int32)
+        return Workload("c4", "paged", dt, q, kc, vc, True,
+                        causal_alignment=causal_alignment or "bottom_right",
+                        kv_indptr=lens_t, k_block_table=kt, v_block_table=vt, kv_page_size=PAGE,
+                        q_lens=[QL] * B, kv_lens=ctx, q_heads=Hq, kv_heads=Hkv, head_dim=D)
+    if name == "c5":
+        dt = dtype or torch.bfloat16
+        B, Hq, Hkv, M, N, D = 4, 32, 1, 1024, 16384, 128
+        q = _randn(gen, (B, Hq, M, D), dt)
+        k = _randn(gen, (B, Hkv, N, D), dt)
+        v = _randn(gen, (B, Hkv, N, D), dt)
+        return Workload("c5", "dense", dt, q, k, v, False, q_lens=[M] * B, kv_lens=[N] * B,
+                        q_heads=Hq, kv_heads=Hkv, head_dim=D)
+    raise KeyError(name)
+
+
+def sequences(w: Workload):
+    """Per-sequence [L,H,D] views (q, k, v lists) of a workload, for the SDPA oracle."""
+    qs, ks, vs = [], [], []
+    B = len(w.q_lens)
+    for b in range(B):
+        if w.layout == "dense":
+            qs.append(w.q[b].transpose(0, 1))
+            ks.append(w.k[b].transpose(0, 1))
+            vs.append(w.v[b].transpose(0, 1))
+        elif w.layout == "ragged":
+            qa, qb = int(w.q_indptr[b]), int(w.q_indptr[b + 1])
+            ka, kb = int(w.kv_indptr[b]), int(w.kv_indptr[b + 1])
+            qs.append(w.q[qa:qb])
+            ks.append(w.k[ka:kb])
+            vs.append(w.v[ka:kb])
+        else:
+            qs.append(w.q[b].transpose(0, 1))
+            ks.append(_gather_one(w.k, w.k_block_table[b], w.kv_lens[b], w.kv_page_size))
+            vs.append(_gather_one(w.v, w.v_block_table[b], w.kv_lens[b], w.kv_page_size))
+    return qs, ks, vs
+
+
+def _gather_one(cache, table_row, n, page):
+    idx = torch.arange(n, device=cache.device)
+    rows = table_row.to(cache.device).long()[idx // page] * page + idx % page
+    return cache[rows]
+
+
+def split_output(w: Workload, out: torch.Tensor):
+    """Per-sequence [L,H,D] views of a layout-shaped output."""
+    res = []
+    for b in range(len(w.q_lens)):
+        if w.layout == "ragged":
+            a, e = int(w.q_indptr[b]), int(w.q_indptr[b + 1])
+            res.append(out[a:e])
+        else:
+            res.append(out[b, :, : w.q_lens[b]].transpose(0, 1))
+    return res
