@@ -88,8 +88,10 @@ def pack(case: Case, layout: str, device="cpu", shuffled_pages=False, seed=0, pa
         q = W.pack_dense(case.qs, max(case.q_lens))
         if shuffled_pages:
             g = torch.Generator().manual_seed(seed + 7)
+            # same pool size (the wrapper asserts equal cache lengths,
+            # attention.py:820), independent page orders
             k, kt = W.paged_cache_shuffled(case.ks, page, 5, g)
-            v, vt = W.paged_cache_shuffled(case.vs, page, 3, g)
+            v, vt = W.paged_cache_shuffled(case.vs, page, 5, g)
         else:
             k, kt = W.paged_cache_contiguous(case.ks, page)
             v, vt = W.paged_cache_contiguous(case.vs, page)
