@@ -93,8 +93,9 @@ typedef struct fa2_params {
   int64_t kv_heads;   /* Hkv, Hq % Hkv == 0; q head h reads kv head h*Hkv/Hq  */
   int64_t head_dim;   /* D                                                     */
   int64_t q_len;      /* dense/paged: M (rows per sequence); ragged: Tq       */
-  int64_t kv_len;     /* dense: N; ragged: Tkv; paged: unused (lengths come
-                         from kv_indptr)                                       */
+  int64_t kv_len;     /* dense: N; ragged: Tkv; paged: rows of the k/v caches
+                         (pages*page_size), or 0 if unknown - per-sequence
+                         lengths always come from kv_indptr                    */
 
   /* Element strides.  Dense/paged q and o use (batch, head, row); ragged q/o
    * and every token-major k/v use (token, head) and ignore *_sb. */

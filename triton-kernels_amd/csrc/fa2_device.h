@@ -15,12 +15,18 @@
 //   * K tiles are staged row-major in LDS, V tiles transposed ([dim][key],
 //     keys permuted inside each 16-key chunk) so that the P^T fragment produced
 //     by the S^T MFMA is consumed by the PV MFMA straight from registers;
-//   * K/V tiles are double-buffered in LDS, the next tile's global loads are
-//     in flight while the current tile is on the MFMA pipes;
-//   * exp is v_exp_f32 (2^x) with scale*log2(e) folded into one FMA;
+//   * software pipeline: K runs one tile ahead of V, so the S MFMAs of tile
+//     t+1 are issued in the same basic block as the softmax VALU work of tile
+//     t; the global loads of K(t+2) and V(t+1) are in flight meanwhile and
+//     land in the other half of the double-buffered LDS;
+//   * K/V rows are read with buffer loads whose hardware range check returns
+//     zeros past the sequence end (no per-row branches); the descriptor is
+//     rebased per tile on the scalar unit;
+//   * exp is v_exp_f32 (2^x) with scale*log2(e) folded into one FMA; the
+//     O rescale is skipped unless a row max grew by more than 2^8 (the
+//     stale max is shared by O and the row sum, so the result is exact);
 //   * causal: tiles past the diagonal are never loaded, masks are evaluated
-//     only on diagonal / sequence-end tiles, and a wave skips a tile that is
-//     fully masked for its 32 rows;
+//     only on diagonal / sequence-end tiles;
 //   * dense causal launches the heaviest q-blocks first; ragged and paged
 //     launches read a heaviest-first work list built on the device by
 //     fa2_plan_kernel (no host synchronisation, unlike attention.py:847).
@@ -28,6 +34,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "fa2.h"
 
@@ -50,6 +58,9 @@ constexpr int kWaveRows = 32;  // query rows per wave
 constexpr int kBN = 64;        // keys per KV tile
 constexpr int kCostBuckets = 4096;
 constexpr int kPlanThreads = 1024;
+constexpr float kRescaleThreshold = 8.0f;  // log2 units: P <= 2^8 between rescales
+// buffer descriptor word 3 for gfx9-family raw (stride 0) buffers, 32-bit data format
+constexpr int kBufferFlags = 0x00020000;
 
 // ---------------------------------------------------------------------------
 // Kernel arguments (one POD passed by value).
@@ -69,11 +80,13 @@ struct KArgs {
   int64_t o_sb, o_sh, o_ss;
   int64_t k_table_stride, v_table_stride;
   int32_t batch, hq, hkv, q_len, kv_len, page_size;
-  int32_t nqb;          // dense: q-blocks per sequence; paged: same
+  int32_t nqb;          // dense/paged: q-blocks per sequence
   int32_t work_ub;      // ragged/paged: capacity of the work list
   int32_t mask;         // enum fa2_mask
   int32_t num_splits;   // >= 1
   float scale_log2;     // softmax_scale * log2(e)
+  uint32_t pool_bytes_k;  // paged + buffer path: bytes of the k cache from the kv-head 0 row 0
+  uint32_t pool_bytes_v;
   const int2* work;     // ragged/paged work list (b, q-block), heaviest first
   const int32_t* work_count;
   float* part_ml;       // split partials: (m, l) per row
@@ -143,6 +156,13 @@ __device__ __forceinline__ void load_raw8(Raw8<DT>& r, const void* base, int64_t
 }
 
 template <int DT>
+__device__ __forceinline__ void buf_raw8(Raw8<DT>& r, __amdgpu_buffer_rsrc_t rs, uint32_t voff) {
+  r.w[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0));
+  if constexpr (DT == FA2_DTYPE_F32)
+    r.w[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16, 0, 0));
+}
+
+template <int DT>
 __device__ __forceinline__ void zero_raw8(Raw8<DT>& r) {
 #pragma unroll
   for (int i = 0; i < Elt<DT>::kBytes / 2; ++i) r.w[i] = (u32x4){0u, 0u, 0u, 0u};
@@ -163,6 +183,11 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kBufferFlags);
+}
+
 // ---------------------------------------------------------------------------
 // Work decoding: workgroup id -> (sequence, head, q-block) and addressing.
 // ---------------------------------------------------------------------------
@@ -171,10 +196,8 @@ struct Work {
   int b, h, kvh, qblk;
   int Lq, Lk;
   int64_t q_base, o_base;  // element offset of row 0 of this (sequence, head)
-  int64_t q_rs, o_rs;      // row strides
   int64_t k_base, v_base;  // dense/ragged: row 0 of this (sequence, kv head);
                            // paged: kv-head offset only
-  int64_t k_rs, v_rs;
   int off;                 // causal diagonal offset: key j visible iff j <= i + off
 };
 
@@ -225,10 +248,6 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L) {
   }
   if (w.Lk < 0) w.Lk = 0;
   if (w.Lq < 0) w.Lq = 0;
-  w.q_rs = a.q_ss;
-  w.o_rs = a.o_ss;
-  w.k_rs = a.k_ss;
-  w.v_rs = a.v_ss;
   w.off = (a.mask == FA2_MASK_CAUSAL_BOTTOM_RIGHT) ? (w.Lk - w.Lq) : 0;
   return w;
 }
@@ -262,10 +281,15 @@ __device__ __forceinline__ int vpos(int kk) {
   return (kk & ~15) | (((g & 1) << 3) | ((g >> 1) << 2)) | (kk & 3);
 }
 
-// Global -> register staging of one K/V tile, then register -> LDS.
-template <int DT, int D, int MODE>
+// Global -> register staging of K and V tiles, then register -> LDS.
+// BUF: all byte offsets of the (sequence, kv-head) slice (dense/ragged) or of
+// the page pool (paged) fit in 31 bits; loads are buffer loads whose range
+// check zero-fills rows past the end.  !BUF: 64-bit global loads of rows
+// clamped to the last valid row (finite data, masked by the softmax).
+template <int DT, int D, int MODE, bool BUF>
 struct TileLoader {
-  static constexpr int kTPR = D / 8;                  // threads per K row
+  static constexpr int kEB = Elt<DT>::kBytes;
+  static constexpr int kTPR = D / 8;  // threads per K row
   static constexpr int kRowsPerPass = kThreads / kTPR;
   static constexpr int kKPasses = kBN / kRowsPerPass;
   static constexpr int kKPT = kBN * D / (8 * kThreads);  // V keys per thread
@@ -273,81 +297,126 @@ struct TileLoader {
 
   Raw8<DT> kr[kKPasses];
   Raw8<DT> vr[kKPT];
+  int krow0, vkey0, col;  // this thread's first K row, first V key, column (elements)
 
-  __device__ __forceinline__ static int64_t paged_row(const int32_t* table, int64_t tstride,
-                                                      int b, int n, int page) {
+  __device__ __forceinline__ TileLoader(int tid) {
+    krow0 = tid / kTPR;
+    col = (tid % kTPR) * 8;
+    vkey0 = (tid / kTPR) * kKPT;
+  }
+
+  __device__ __forceinline__ static int paged_row(const int32_t* table, int64_t tstride, int b,
+                                                  int n, int page) {
     const int pg = table[b * tstride + n / page];
-    return static_cast<int64_t>(pg) * page + (n % page);
+    return pg * page + (n % page);
   }
 
-  __device__ __forceinline__ void issue(const KArgs& a, const Work& w, int k0, int tid) {
-    // K: row-major rows, 8 elements per thread per pass.
-    const int kcol = (tid % kTPR) * 8;
+  __device__ __forceinline__ void issue_k(const KArgs& a, const Work& w, int k0) {
+    if constexpr (BUF) {
+      if constexpr (MODE == FA2_LAYOUT_PAGED) {
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(static_cast<const char*>(a.k) + w.k_base * kEB, a.pool_bytes_k);
 #pragma unroll
-    for (int p = 0; p < kKPasses; ++p) {
-      const int n = k0 + tid / kTPR + p * kRowsPerPass;
-      if (n < w.Lk) {
-        int64_t off;
-        if constexpr (MODE == FA2_LAYOUT_PAGED)
-          off = w.k_base + paged_row(a.k_table, a.k_table_stride, w.b, n, a.page_size) * w.k_rs;
-        else
-          off = w.k_base + static_cast<int64_t>(n) * w.k_rs;
-        load_raw8<DT>(kr[p], a.k, off + kcol);
+        for (int p = 0; p < kKPasses; ++p) {
+          const int n = k0 + krow0 + p * kRowsPerPass;
+          const int nc = min(n, w.Lk - 1);
+          const uint32_t row = paged_row(a.k_table, a.k_table_stride, w.b, nc, a.page_size);
+          const uint32_t off = row * static_cast<uint32_t>(a.k_ss * kEB) + col * kEB;
+          buf_raw8<DT>(kr[p], rs, n < w.Lk ? off : 0xFFFFFF00u);
+        }
       } else {
-        zero_raw8<DT>(kr[p]);
+        const uint32_t rsb = static_cast<uint32_t>(a.k_ss * kEB);
+        const uint32_t lim = static_cast<uint32_t>(w.Lk - k0) * rsb;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+            static_cast<const char*>(a.k) + (w.k_base + static_cast<int64_t>(k0) * a.k_ss) * kEB,
+            lim);
+#pragma unroll
+        for (int p = 0; p < kKPasses; ++p)
+          buf_raw8<DT>(kr[p], rs, (krow0 + p * kRowsPerPass) * rsb + col * kEB);
       }
-    }
-    // V: kKPT consecutive keys x 8 dims per thread.
-    const int vcol = (tid % kTPR) * 8;
-    const int vkey = (tid / kTPR) * kKPT;
+    } else {
 #pragma unroll
-    for (int j = 0; j < kKPT; ++j) {
-      const int n = k0 + vkey + j;
-      if (n < w.Lk) {
+      for (int p = 0; p < kKPasses; ++p) {
+        const int n = min(k0 + krow0 + p * kRowsPerPass, w.Lk - 1);
         int64_t off;
         if constexpr (MODE == FA2_LAYOUT_PAGED)
-          off = w.v_base + paged_row(a.v_table, a.v_table_stride, w.b, n, a.page_size) * w.v_rs;
+          off = w.k_base +
+                static_cast<int64_t>(paged_row(a.k_table, a.k_table_stride, w.b, n, a.page_size)) *
+                    a.k_ss;
         else
-          off = w.v_base + static_cast<int64_t>(n) * w.v_rs;
-        load_raw8<DT>(vr[j], a.v, off + vcol);
-      } else {
-        zero_raw8<DT>(vr[j]);
+          off = w.k_base + static_cast<int64_t>(n) * a.k_ss;
+        load_raw8<DT>(kr[p], a.k, off + col);
       }
     }
   }
 
-  __device__ __forceinline__ void commit(uint16_t* ks, uint16_t* vt, int tid) const {
+  __device__ __forceinline__ void issue_v(const KArgs& a, const Work& w, int k0) {
+    if constexpr (BUF) {
+      if constexpr (MODE == FA2_LAYOUT_PAGED) {
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(static_cast<const char*>(a.v) + w.v_base * kEB, a.pool_bytes_v);
+#pragma unroll
+        for (int j = 0; j < kKPT; ++j) {
+          const int n = k0 + vkey0 + j;
+          const int nc = min(n, w.Lk - 1);
+          const uint32_t row = paged_row(a.v_table, a.v_table_stride, w.b, nc, a.page_size);
+          const uint32_t off = row * static_cast<uint32_t>(a.v_ss * kEB) + col * kEB;
+          buf_raw8<DT>(vr[j], rs, n < w.Lk ? off : 0xFFFFFF00u);
+        }
+      } else {
+        const uint32_t rsb = static_cast<uint32_t>(a.v_ss * kEB);
+        const uint32_t lim = static_cast<uint32_t>(w.Lk - k0) * rsb;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+            static_cast<const char*>(a.v) + (w.v_base + static_cast<int64_t>(k0) * a.v_ss) * kEB,
+            lim);
+#pragma unroll
+        for (int j = 0; j < kKPT; ++j) buf_raw8<DT>(vr[j], rs, (vkey0 + j) * rsb + col * kEB);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kKPT; ++j) {
+        const int n = min(k0 + vkey0 + j, w.Lk - 1);
+        int64_t off;
+        if constexpr (MODE == FA2_LAYOUT_PAGED)
+          off = w.v_base +
+                static_cast<int64_t>(paged_row(a.v_table, a.v_table_stride, w.b, n, a.page_size)) *
+                    a.v_ss;
+        else
+          off = w.v_base + static_cast<int64_t>(n) * a.v_ss;
+        load_raw8<DT>(vr[j], a.v, off + col);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void commit_k(uint16_t* ks) const {
     using L = Lds<D>;
-    const int kcol = (tid % kTPR) * 8;
 #pragma unroll
     for (int p = 0; p < kKPasses; ++p) {
-      const int row = tid / kTPR + p * kRowsPerPass;
-      *reinterpret_cast<u32x4*>(ks + row * L::kKStride + kcol) = to16<DT>(kr[p]);
+      const int row = krow0 + p * kRowsPerPass;
+      *reinterpret_cast<u32x4*>(ks + row * L::kKStride + col) = to16<DT>(kr[p]);
     }
-    const int vcol = (tid % kTPR) * 8;
-    const int vkey = (tid / kTPR) * kKPT;
+  }
+
+  __device__ __forceinline__ void commit_v(uint16_t* vt) const {
+    using L = Lds<D>;
     u32x4 x[kKPT];
 #pragma unroll
     for (int j = 0; j < kKPT; ++j) x[j] = to16<DT>(vr[j]);
-    const int pos = vpos(vkey);  // kKPT <= 4 consecutive keys stay adjacent
+    const int pos = vpos(vkey0);  // kKPT <= 4 consecutive keys stay adjacent
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const int word = d >> 1;
-      const bool hi = d & 1;
-      uint16_t* dst = vt + (vcol + d) * L::kVStride + pos;
+      // v_perm_b32 byte selectors: low halves (d even) or high halves (d odd)
+      const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+      uint16_t* dst = vt + (col + d) * L::kVStride + pos;
       if constexpr (kKPT == 4) {
-        uint32_t e0 = hi ? (x[0][word] >> 16) : (x[0][word] & 0xffffu);
-        uint32_t e1 = hi ? (x[1][word] >> 16) : (x[1][word] & 0xffffu);
-        uint32_t e2 = hi ? (x[2][word] >> 16) : (x[2][word] & 0xffffu);
-        uint32_t e3 = hi ? (x[3][word] >> 16) : (x[3][word] & 0xffffu);
-        *reinterpret_cast<u32x2*>(dst) = (u32x2){e0 | (e1 << 16), e2 | (e3 << 16)};
+        const uint32_t a01 = __builtin_amdgcn_perm(x[1][word], x[0][word], sel);
+        const uint32_t a23 = __builtin_amdgcn_perm(x[3][word], x[2][word], sel);
+        *reinterpret_cast<u32x2*>(dst) = (u32x2){a01, a23};
       } else if constexpr (kKPT == 2) {
-        uint32_t e0 = hi ? (x[0][word] >> 16) : (x[0][word] & 0xffffu);
-        uint32_t e1 = hi ? (x[1][word] >> 16) : (x[1][word] & 0xffffu);
-        *reinterpret_cast<uint32_t*>(dst) = e0 | (e1 << 16);
+        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(x[1][word], x[0][word], sel);
       } else {
-        uint32_t e0 = hi ? (x[0][word] >> 16) : (x[0][word] & 0xffffu);
-        *dst = static_cast<uint16_t>(e0);
+        *dst = static_cast<uint16_t>((d & 1) ? (x[0][word] >> 16) : (x[0][word] & 0xffffu));
       }
     }
   }
@@ -356,7 +425,18 @@ struct TileLoader {
 // ---------------------------------------------------------------------------
 // Forward kernel.
 // ---------------------------------------------------------------------------
-template <int DT, int D, int MODE>
+// S of the next tile is software-pipelined against the softmax of the current
+// one where the registers allow it (two waves per SIMD = 256 VGPRs).
+template <int D>
+struct Pipe {
+#ifdef FA2_PIPE_D128
+  static constexpr bool value = true;
+#else
+  static constexpr bool value = D <= 64;
+#endif
+};
+
+template <int DT, int D, int MODE, bool BUF, bool PIPE = Pipe<D>::value>
 __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
   constexpr bool BF = Elt<DT>::kBF;
   constexpr int DC = D / 16;  // 16-wide head-dim chunks of Q^T (MFMA k-steps)
@@ -383,13 +463,14 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
   const int ntiles = (kv_end + kBN - 1) / kBN;
   const int t_begin = (ntiles * split) / S;
   const int t_end = (ntiles * (split + 1)) / S;
+  const int T = t_end - t_begin;
 
   // Q^T fragments: lane holds query row q0 + 32*wave + l32, dims c*16+8*hi..+7.
   const int qrow = q0 + wave * kWaveRows + l32;
   u32x4 qf[DC];
   {
     const bool ok = qrow < w.Lq;
-    const int64_t base = w.q_base + static_cast<int64_t>(qrow) * w.q_rs + hi * 8;
+    const int64_t base = w.q_base + static_cast<int64_t>(qrow) * a.q_ss + hi * 8;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       Raw8<DT> r;
@@ -409,110 +490,142 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
 
   uint16_t* ks_base = lds;
   uint16_t* vt_base = lds + 2 * L::kKTile;
-
-  // first (wave-row) query index and the last one of this wave
   const int wq_first = q0 + wave * kWaveRows;
-  const int wq_last = wq_first + kWaveRows - 1;
   const bool causal = a.mask != FA2_MASK_NONE;
 
-  TileLoader<DT, D, MODE> ld;
-  if (t_begin < t_end) {
-    ld.issue(a, w, t_begin * kBN, tid);
-    ld.commit(ks_base, vt_base, tid);
-  }
-  __syncthreads();
+  TileLoader<DT, D, MODE, BUF> ld(tid);
 
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
+  // S^T block for the tile held in K buffer `kb`.
+  auto compute_s = [&](f32x16 (&s)[SB], int kb) {
+    const uint16_t* ks = ks_base + kb * L::kKTile;
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+      s[sb] = (f32x16){};
+      const uint16_t* krow = ks + (sb * 32 + l32) * L::kKStride + hi * 8;
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + c * 16);
+        s[sb] = mma32<BF>(kf, qf[c], s[sb]);
+      }
+    }
+  };
+
+  // One pipeline step: softmax + PV of tile i (scores in s_cur), S of tile
+  // i+1 into s_nxt, loads of K(i+2) and V(i+1).  `last` (a compile-time
+  // flag) marks the final tile, which has no successor.
+  auto step = [&](auto last, int i, f32x16 (&s_cur)[SB], f32x16 (&s_nxt)[SB]) {
+    constexpr bool kLast = decltype(last)::value;
+    const int t = t_begin + i;
     const int k0 = t * kBN;
-    const bool more = (t + 1) < t_end;
-    if (more) ld.issue(a, w, k0 + kBN, tid);
+    constexpr bool has_next = !kLast;
+    // PIPE: K runs two tiles ahead (S of tile t+1 is computed in this step);
+    // otherwise K and V both run one tile ahead and S(t) is computed here.
+    const bool has_k2 = PIPE ? (!kLast && (i + 2 < T)) : has_next;
+    if (has_k2) ld.issue_k(a, w, k0 + (PIPE ? 2 : 1) * kBN);
+    if constexpr (has_next) ld.issue_v(a, w, k0 + kBN);
+    if constexpr (!PIPE) compute_s(s_cur, i & 1);
 
-    const uint16_t* ks = ks_base + buf * L::kKTile;
-    const uint16_t* vt = vt_base + buf * L::kVTile;
-
-    // wave-uniform: does this tile hold any visible key for this wave's rows?
-    const bool wave_live = !causal || (k0 <= wq_last + w.off);
-    if (wave_live) {
-      // S^T = K Q^T for 64 keys x 32 queries.
-      f32x16 s[SB];
+    // masks only at the sequence end or on the causal diagonal (wave-uniform)
+    if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
-        s[sb] = (f32x16){};
-        const uint16_t* krow = ks + (sb * 32 + l32) * L::kKStride + hi * 8;
 #pragma unroll
-        for (int c = 0; c < DC; ++c) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + c * 16);
-          s[sb] = mma32<BF>(kf, qf[c], s[sb]);
-        }
-      }
-      // Mask only where needed: sequence end or the causal diagonal.
-      const bool need_mask = (k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off));
-      if (need_mask) {
-        const int qi = qrow;
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = k0 + sb * 32 + (i >> 2) * 8 + hi * 4 + (i & 3);
-            const bool ok = (key < w.Lk) && (!causal || key <= qi + w.off);
-            if (!ok) s[sb][i] = -INFINITY;
-          }
-        }
-      }
-      // Online softmax (row = this lane's query).
-      float mx = -INFINITY;
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
-      mx = fmaxf(mx, xor32(mx));
-      const float m_new = fmaxf(m_run, mx * a.scale_log2);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-      float rs = 0.f;
-      u32x4 pf[kBN / 16];
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-        float p[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          p[i] = fast_exp2(__builtin_fmaf(s[sb][i], a.scale_log2, -m_use));
-          rs += p[i];
-        }
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          pf[sb * 2 + half] = (u32x4){pack2<BF>(p[half * 8 + 0], p[half * 8 + 1]),
-                                      pack2<BF>(p[half * 8 + 2], p[half * 8 + 3]),
-                                      pack2<BF>(p[half * 8 + 4], p[half * 8 + 5]),
-                                      pack2<BF>(p[half * 8 + 6], p[half * 8 + 7])};
-        }
-      }
-      l_run = l_run * alpha + rs;
-#pragma unroll
-      for (int d = 0; d < DB; ++d) o[d] *= alpha;
-      // O^T += V^T P^T
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        const uint16_t* vrow = vt + (d * 32 + l32) * L::kVStride + hi * 8;
-#pragma unroll
-        for (int c = 0; c < kBN / 16; ++c) {
-          const u32x4 vf = *reinterpret_cast<const u32x4*>(vrow + c * 16);
-          o[d] = mma32<BF>(vf, pf[c], o[d]);
+        for (int i2 = 0; i2 < 16; ++i2) {
+          const int key = k0 + sb * 32 + (i2 >> 2) * 8 + hi * 4 + (i2 & 3);
+          const bool ok = (key < w.Lk) && (!causal || key <= qrow + w.off);
+          if (!ok) s_cur[sb][i2] = -INFINITY;
         }
       }
     }
 
-    if (more) ld.commit(ks_base + (buf ^ 1) * L::kKTile, vt_base + (buf ^ 1) * L::kVTile, tid);
+    if constexpr (has_next && PIPE) compute_s(s_nxt, (i + 1) & 1);
+
+    // online softmax of tile i (row = this lane's query)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) mx = fmaxf(mx, s_cur[sb][i2]);
+    mx = fmaxf(mx, xor32(mx));
+    const float mt = mx * a.scale_log2;
+    const bool need = mt > m_run + kRescaleThreshold;
+    const float alpha = need ? fast_exp2(m_run - mt) : 1.0f;
+    const float m_new = need ? mt : m_run;
+    m_run = m_new;
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    float rs = 0.f;
+    u32x4 pf[kBN / 16];
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+      float p[16];
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) {
+        p[i2] = fast_exp2(__builtin_fmaf(s_cur[sb][i2], a.scale_log2, -m_use));
+        rs += p[i2];
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        pf[sb * 2 + half] = (u32x4){pack2<BF>(p[half * 8 + 0], p[half * 8 + 1]),
+                                    pack2<BF>(p[half * 8 + 2], p[half * 8 + 3]),
+                                    pack2<BF>(p[half * 8 + 4], p[half * 8 + 5]),
+                                    pack2<BF>(p[half * 8 + 6], p[half * 8 + 7])};
+      }
+    }
+    l_run = l_run * alpha + rs;
+    if (__any(need)) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) o[d] *= alpha;
+    }
+    // O^T += V^T P^T
+    const uint16_t* vt = vt_base + (i & 1) * L::kVTile;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const uint16_t* vrow = vt + (d * 32 + l32) * L::kVStride + hi * 8;
+#pragma unroll
+      for (int c = 0; c < kBN / 16; ++c) {
+        const u32x4 vf = *reinterpret_cast<const u32x4*>(vrow + c * 16);
+        o[d] = mma32<BF>(vf, pf[c], o[d]);
+      }
+    }
+    if (has_k2) ld.commit_k(ks_base + ((PIPE ? i : i + 1) & 1) * L::kKTile);
+    if constexpr (has_next) {
+      ld.commit_v(vt_base + ((i + 1) & 1) * L::kVTile);
+      __syncthreads();
+    }
+  };
+  using NotLast = std::integral_constant<bool, false>;
+  using Last = std::integral_constant<bool, true>;
+
+  f32x16 sA[SB], sB[SB];
+  if (T > 0) {
+    ld.issue_k(a, w, t_begin * kBN);
+    ld.issue_v(a, w, t_begin * kBN);
+    ld.commit_k(ks_base);
+    ld.commit_v(vt_base);
+    if (PIPE && T > 1) {
+      ld.issue_k(a, w, (t_begin + 1) * kBN);
+      ld.commit_k(ks_base + L::kKTile);
+    }
     __syncthreads();
+    if constexpr (PIPE) compute_s(sA, 0);
+    int i = 0;
+    for (; i + 2 < T; i += 2) {
+      step(NotLast{}, i, sA, sB);
+      step(NotLast{}, i + 1, sB, sA);
+    }
+    if (i + 1 < T) {
+      step(NotLast{}, i, sA, sB);
+      step(Last{}, i + 1, sB, sA);
+    } else {
+      step(Last{}, i, sA, sB);
+    }
   }
 
   const float l_tot = l_run + xor32(l_run);
   if (S == 1) {
     if (qrow < w.Lq) {
       const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
-      const int64_t base = w.o_base + static_cast<int64_t>(qrow) * w.o_rs + hi * 4;
+      const int64_t base = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + hi * 4;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -583,7 +696,7 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
       acc += wgt * x;
     }
     const float inv = 1.f / lsum;
-    const int64_t off = w.o_base + static_cast<int64_t>(qrow) * w.o_rs + col;
+    const int64_t off = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + col;
     if constexpr (DT == FA2_DTYPE_F32) {
       *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + off) = acc * inv;
     } else {

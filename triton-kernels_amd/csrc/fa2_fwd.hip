@@ -15,6 +15,7 @@
 #include <mutex>
 
 #include "fa2_device.h"
+#include "fa2_kernel_lds.h"
 
 namespace fa2 {
 namespace {
@@ -49,8 +50,26 @@ struct Plan {
   int64_t work_ub;  // (sequence, q-block) slots
   int64_t grid_x;   // work_ub * Hq
   int splits;
+  bool buf;         // K/V byte offsets fit the 31-bit buffer-load path
+  uint32_t pool_bytes_k, pool_bytes_v;
   size_t off_work, off_count, off_ml, off_o, total;
 };
+
+// Buffer loads address a K/V slice with 32-bit offsets and a range check.
+// Dense/ragged: the (sequence, kv head) slice is at most kv_len rows; paged:
+// the whole pool of kv_len rows.  Rows must not overlap (stride >= D).
+bool buffer_path_ok(const fa2_params* p, uint32_t* kbytes, uint32_t* vbytes) {
+  const int64_t eb = elt_bytes(p->dtype);
+  const int64_t lim = (int64_t(1) << 31) - 1024;
+  if (p->kv_len <= 0) return false;
+  if (p->k_ss < p->head_dim || p->v_ss < p->head_dim) return false;
+  const int64_t kb = p->kv_len * p->k_ss * eb;
+  const int64_t vb = p->kv_len * p->v_ss * eb;
+  if (kb > lim || vb > lim) return false;
+  *kbytes = static_cast<uint32_t>(kb);
+  *vbytes = static_cast<uint32_t>(vb);
+  return true;
+}
 
 int validate(const fa2_params* p) {
   if (!p) return FA2_ERR_NULL_POINTER;
@@ -115,6 +134,8 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     }
   }
   pl->splits = splits;
+  pl->pool_bytes_k = pl->pool_bytes_v = 0;
+  pl->buf = buffer_path_ok(p, &pl->pool_bytes_k, &pl->pool_bytes_v);
 
   size_t off = 0;
   pl->off_work = off;
@@ -138,8 +159,19 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
     hipLaunchKernelGGL((fa2_plan_kernel<MODE>), dim3(1), dim3(kPlanThreads), 0, st, a,
                        const_cast<int2*>(a.work), const_cast<int32_t*>(a.work_count));
   }
-  hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE>), dim3(pl.grid_x, pl.splits), dim3(kThreads), 0,
-                     st, a);
+  const dim3 grid(pl.grid_x, pl.splits);
+  if constexpr (DT == FA2_DTYPE_F32) {
+    if (pl.buf)
+      hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st, a);
+  } else {
+    if (pl.buf)
+      hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st,
+                         a);
+  }
   if (pl.splits > 1) {
     hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), dim3(pl.grid_x), dim3(kThreads), 0, st,
                        a);
@@ -244,6 +276,8 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
   a.mask = p->mask;
   a.num_splits = pl.splits;
   a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+  a.pool_bytes_k = pl.pool_bytes_k;
+  a.pool_bytes_v = pl.pool_bytes_v;
   char* ws = static_cast<char*>(p->workspace);
   a.work = p->layout != FA2_LAYOUT_DENSE ? reinterpret_cast<const int2*>(ws + pl.off_work) : nullptr;
   a.work_count =

@@ -1,0 +1,415 @@
+// fa2_kernel_lds.h - fp16/bf16 forward kernel with direct HBM->LDS tiles.
+//
+// Same math and work decomposition as the register-staged kernel in
+// fa2_device.h (which remains the fp32 path), with the tile traffic moved
+// off the VALU:
+//   * K and V tiles are written to LDS by `buffer_load_dwordx4 ... lds`
+//     (gfx950 direct-to-LDS, 16 bytes per lane): no staging registers, no
+//     ds_write; out-of-range rows read as zeros through the buffer range
+//     check (dense/ragged) or a range-violating offset (paged);
+//   * rows are stored unpadded with an XOR swizzle of their 16-byte chunks,
+//     chosen so that both the ds_read_b128 of K (one row per lane) and the
+//     ds_read_b64_tr_b16 of V hit distinct banks;
+//   * V stays row-major: ds_read_b64_tr_b16 transposes 4 keys x 16 dims per
+//     16-lane group, so two of them give the V^T MFMA operand (one head dim
+//     and 8 keys per lane) in the key order of the P^T fragment;
+//   * the S MFMAs of tile t+1 share a basic block with the softmax of tile t.
+#pragma once
+
+#include "fa2_device.h"
+
+namespace fa2 {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) char lds_char_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4_t;
+
+// Row geometry and swizzles (16-byte chunk units) for a head dim D.
+template <int D>
+struct SwzGeo {
+  static constexpr int kNC = D / 8;          // chunks per row
+  static constexpr int kRowBytes = D * 2;
+  static constexpr int kTileBytes = kBN * kRowBytes;
+  // K rows are read one row per lane (16 lanes per bank cycle): 16 rows
+  // must land on 16 distinct chunk slots of a 256-byte bank window.
+  __device__ __forceinline__ static int k(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+  // V rows are read 4 rows x 4 chunks per 32 lanes by the transpose read.
+  __device__ __forceinline__ static int v(int r) {
+    return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
+  }
+};
+
+__device__ __forceinline__ lds_char_t* to_lds(void* p) {
+  return (lds_char_t*)((__attribute__((address_space(3))) uint16_t*)(uint16_t*)p);
+}
+
+// Direct-to-LDS loads are issued through inline asm: the compiler then does
+// not see an asynchronous LDS write and cannot serialise every later LDS read
+// behind it (it cannot tell the double-buffer halves apart).  Completion is
+// awaited explicitly by lds_fill_barrier() before the buffer is read; the
+// waits the compiler emits for its own loads only get more conservative
+// (vector-memory loads retire in order).
+__device__ __forceinline__ void dma_buffer_x4(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))), "v"(voff), "s"(rsrc)
+      : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma_global_x4(const void* gptr, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "global_load_lds_dwordx4 %1, off"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))), "v"(gptr)
+      : "memory", "m0");
+}
+
+// Buffer descriptor as four SGPR words (base, stride 0, num_records, flags).
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t w0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b)));
+  const uint32_t w1 = static_cast<uint32_t>(
+      __builtin_amdgcn_readfirstlane(static_cast<int>((b >> 32) & 0xFFFFu)));
+  const uint32_t w2 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(bytes)));
+  return (u32x4){w0, w1, w2, static_cast<uint32_t>(kBufferFlags)};
+}
+
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(const_cast<void*>(p))));
+}
+
+template <int D, int MODE, bool BUF, int DT>
+struct DirectLoader {
+  using G = SwzGeo<D>;
+  static constexpr int kEB = 2;
+  static constexpr int kInstr = G::kNC / 4;  // 1 KiB wave instructions per tensor per tile
+  static_assert(kInstr >= 1, "head dim");
+
+  // dense/ragged: byte offset (row * stride + swizzled chunk) of this lane's
+  // slot for instruction j, relative to the tile's first row
+  uint32_t kvo[kInstr], vvo[kInstr];
+  int wave, lane;
+
+  // tile row and 16-byte slot of this lane for wave instruction j
+  __device__ __forceinline__ int row_of(int j) const {
+    return ((wave * kInstr + j) * 64 + lane) / G::kNC;
+  }
+  __device__ __forceinline__ int slot_of() const { return lane % G::kNC; }
+
+  __device__ __forceinline__ DirectLoader(const KArgs& a, int tid) {
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+    if constexpr (MODE != FA2_LAYOUT_PAGED) {
+      const uint32_t krs = static_cast<uint32_t>(a.k_ss * kEB);
+      const uint32_t vrs = static_cast<uint32_t>(a.v_ss * kEB);
+#pragma unroll
+      for (int j = 0; j < kInstr; ++j) {
+        const int r = row_of(j);
+        kvo[j] = r * krs + ((slot_of() ^ G::k(r)) * 16);
+        vvo[j] = r * vrs + ((slot_of() ^ G::v(r)) * 16);
+      }
+    }
+  }
+
+  __device__ __forceinline__ static int paged_row(const int32_t* table, int64_t tstride, int b,
+                                                  int n, int page) {
+    const int pg = table[b * tstride + n / page];
+    return pg * page + (n % page);
+  }
+
+  // Issue the loads of one tile of K (IS_V=false) or V into `dst`.
+  template <bool IS_V>
+  __device__ __forceinline__ void issue(const KArgs& a, const Work& w, int k0, void* dst) const {
+    const void* src = IS_V ? a.v : a.k;
+    const int64_t rs = IS_V ? a.v_ss : a.k_ss;
+    const int64_t base = IS_V ? w.v_base : w.k_base;
+    const uint32_t ldst = lds_addr_of(dst) + wave * kInstr * 1024;
+    if constexpr (BUF) {
+      const uint32_t rsb = static_cast<uint32_t>(rs * kEB);
+      if constexpr (MODE == FA2_LAYOUT_PAGED) {
+        const u32x4 rsrc = rsrc_words(static_cast<const char*>(src) + base * kEB,
+                                      IS_V ? a.pool_bytes_v : a.pool_bytes_k);
+        const int32_t* tbl = IS_V ? a.v_table : a.k_table;
+        const int64_t ts = IS_V ? a.v_table_stride : a.k_table_stride;
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+          const int r = row_of(j);
+          const int n = k0 + r;
+          const int nc = min(n, w.Lk - 1);
+          const uint32_t prow = static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
+          const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
+          dma_buffer_x4(rsrc, ldst + j * 1024, n < w.Lk ? prow * rsb + col : 0xFFFFFF00u);
+        }
+      } else {
+        const uint32_t lim = static_cast<uint32_t>(w.Lk - k0) * rsb;
+        const u32x4 rsrc = rsrc_words(
+            static_cast<const char*>(src) + (base + static_cast<int64_t>(k0) * rs) * kEB, lim);
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j)
+          dma_buffer_x4(rsrc, ldst + j * 1024, IS_V ? vvo[j] : kvo[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kInstr; ++j) {
+        const int r = row_of(j);
+        const int n = min(k0 + r, w.Lk - 1);  // clamped: finite data, masked later
+        int64_t r64;
+        if constexpr (MODE == FA2_LAYOUT_PAGED)
+          r64 = paged_row(IS_V ? a.v_table : a.k_table, IS_V ? a.v_table_stride : a.k_table_stride,
+                          w.b, n, a.page_size);
+        else
+          r64 = n;
+        const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
+        dma_global_x4(static_cast<const char*>(src) + (base + r64 * rs) * kEB + col,
+                      ldst + j * 1024);
+      }
+    }
+  }
+};
+
+// Wait for this wave's outstanding direct-to-LDS loads (vmcnt), then barrier.
+__device__ __forceinline__ void lds_fill_barrier() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+#ifndef FA2_LDS_OCCUPANCY
+#define FA2_LDS_OCCUPANCY 2
+#endif
+// PIPE: K runs two tiles ahead and the S MFMAs of tile t+1 overlap the
+// softmax of tile t; otherwise K runs one tile ahead and S(t) starts step t.
+// Measured on MI355X (bf16, D=128): the pipelined form needs more than the
+// 256 VGPRs of two waves per SIMD and spills; the plain form is faster
+// (c2 669 vs 614 TFLOP/s) while D=64 pipelines without spilling.
+#ifndef FA2_LDS_PIPE
+#define FA2_LDS_PIPE_DEFAULT(D) ((D) <= 64)
+#else
+#define FA2_LDS_PIPE_DEFAULT(D) (FA2_LDS_PIPE != 0)
+#endif
+template <int DT, int D, int MODE, bool BUF, bool PIPE = FA2_LDS_PIPE_DEFAULT(D)>
+__global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kernel(KArgs a) {
+  static_assert(DT != FA2_DTYPE_F32, "fp32 uses the register-staged kernel");
+  constexpr bool BF = Elt<DT>::kBF;
+  constexpr int DC = D / 16;  // MFMA k-steps of S (16 head dims each)
+  constexpr int DB = D / 32;  // 32-dim blocks of O^T
+  constexpr int SB = kBN / 32;
+  using G = SwzGeo<D>;
+
+  __shared__ __attribute__((aligned(1024))) char lds[4 * G::kTileBytes];
+  char* kbuf[2] = {lds, lds + G::kTileBytes};
+  char* vbuf[2] = {lds + 2 * G::kTileBytes, lds + 3 * G::kTileBytes};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+
+  const Work w = decode_work<MODE>(a, blockIdx.x);
+  if (!w.valid) return;
+  const int q0 = w.qblk * kBM;
+  const int split = blockIdx.y;
+  const int S = a.num_splits;
+
+  const int kv_end = kv_end_for_block(a.mask, q0, w.Lq, w.Lk, w.off);
+  const int ntiles = (kv_end + kBN - 1) / kBN;
+  const int t_begin = (ntiles * split) / S;
+  const int t_end = (ntiles * (split + 1)) / S;
+  const int T = t_end - t_begin;
+
+  // Q^T fragments (B operand of S^T = K Q^T): query row q0+32*wave+l32.
+  const int qrow = q0 + wave * kWaveRows + l32;
+  u32x4 qf[DC];
+  {
+    const bool ok = qrow < w.Lq;
+    const int64_t base = w.q_base + static_cast<int64_t>(qrow) * a.q_ss + hi * 8;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      Raw8<DT> r;
+      if (ok)
+        load_raw8<DT>(r, a.q, base + c * 16);
+      else
+        zero_raw8<DT>(r);
+      qf[c] = to16<DT>(r);
+    }
+  }
+
+  // Per-lane LDS byte offsets.  K (A operand of S^T): row sb*32 + l32, chunk
+  // 2*cc + hi.  Both row blocks share the swizzle (32 = 0 mod 16 rows).
+  // The swizzle only flips chunk bits, i.e. address bits below the row
+  // offset, so offset(cc) = offset(0) ^ (32 * cc) for K and
+  // offset(db) = offset(0) ^ (64 * db) for V (one register each).
+  const uint32_t koff0 = l32 * G::kRowBytes + ((hi ^ G::k(l32)) * 16);
+  // V (A operand of O^T via the transpose read): source lane i of 16-lane
+  // group g reads row 16c + 8rr + 4*(g/2) + i/4, dims 32db + 16(g%2) + 4(i%4).
+  uint32_t voff0;
+  {
+    const int g = lane >> 4, i = lane & 15;
+    const int r = 4 * (g >> 1) + (i >> 2);  // + 16c + 8rr (multiples of 8: same swizzle)
+    const int dim = 16 * (g & 1) + 4 * (i & 3);
+    voff0 = r * G::kRowBytes + (((dim >> 3) ^ G::v(r)) * 16) + (dim & 7) * 2;
+  }
+
+  f32x16 o[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) o[d] = (f32x16){};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  const int wq_first = q0 + wave * kWaveRows;
+  const bool causal = a.mask != FA2_MASK_NONE;
+
+  const DirectLoader<D, MODE, BUF, DT> ld(a, tid);
+
+  auto compute_s = [&](f32x16 (&s)[SB], const char* kb) {
+    const lds_char_t* kl = to_lds(const_cast<char*>(kb));
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+      s[sb] = (f32x16){};
+#pragma unroll
+      for (int cc = 0; cc < DC; ++cc) {
+        const u32x4 kf =
+            *(const lds_u32x4_t*)(kl + sb * 32 * G::kRowBytes + (koff0 ^ (32u * cc)));
+        s[sb] = mma32<BF>(kf, qf[cc], s[sb]);
+      }
+    }
+  };
+
+  auto step = [&](auto last, int i, f32x16 (&s_cur)[SB], f32x16 (&s_nxt)[SB]) {
+    constexpr bool kLast = decltype(last)::value;
+    const int t = t_begin + i;
+    const int k0 = t * kBN;
+    if constexpr (!kLast) {
+      if (PIPE ? (i + 2 < T) : true)
+        ld.template issue<false>(a, w, k0 + (PIPE ? 2 : 1) * kBN, kbuf[(PIPE ? i : i + 1) & 1]);
+      ld.template issue<true>(a, w, k0 + kBN, vbuf[(i + 1) & 1]);
+    }
+    if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int i2 = 0; i2 < 16; ++i2) {
+          const int key = k0 + sb * 32 + (i2 >> 2) * 8 + hi * 4 + (i2 & 3);
+          const bool ok = (key < w.Lk) && (!causal || key <= qrow + w.off);
+          if (!ok) s_cur[sb][i2] = -INFINITY;
+        }
+      }
+    }
+    if constexpr (!PIPE) compute_s(s_cur, kbuf[i & 1]);
+    if constexpr (!kLast && PIPE) compute_s(s_nxt, kbuf[(i + 1) & 1]);
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) mx = fmaxf(mx, s_cur[sb][i2]);
+    mx = fmaxf(mx, xor32(mx));
+    const float mt = mx * a.scale_log2;
+    const bool need = mt > m_run + kRescaleThreshold;
+    const float alpha = need ? fast_exp2(m_run - mt) : 1.0f;
+    const float m_new = need ? mt : m_run;
+    m_run = m_new;
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    float rs = 0.f;
+    u32x4 pf[kBN / 16];
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+      float p[16];
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) {
+        p[i2] = fast_exp2(__builtin_fmaf(s_cur[sb][i2], a.scale_log2, -m_use));
+        rs += p[i2];
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+        pf[sb * 2 + half] = (u32x4){pack2<BF>(p[half * 8 + 0], p[half * 8 + 1]),
+                                    pack2<BF>(p[half * 8 + 2], p[half * 8 + 3]),
+                                    pack2<BF>(p[half * 8 + 4], p[half * 8 + 5]),
+                                    pack2<BF>(p[half * 8 + 6], p[half * 8 + 7])};
+    }
+    l_run = l_run * alpha + rs;
+    if (__any(need)) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) o[d] *= alpha;
+    }
+    // O^T += V^T P^T; V^T fragments from two transposed reads per MFMA
+    const lds_char_t* vl = to_lds(vbuf[i & 1]);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const uint32_t voff = voff0 ^ (64u * d);
+#pragma unroll
+      for (int c = 0; c < kBN / 16; ++c) {
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4i16_t*)(vl + (16 * c) * G::kRowBytes + voff));
+        const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4i16_t*)(vl + (16 * c + 8) * G::kRowBytes + voff));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+        const u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
+        o[d] = mma32<BF>((u32x4){l2[0], l2[1], h2[0], h2[1]}, pf[c], o[d]);
+      }
+    }
+    if constexpr (!kLast) lds_fill_barrier();
+  };
+  using NotLast = std::integral_constant<bool, false>;
+  using Last = std::integral_constant<bool, true>;
+
+  f32x16 sA[SB], sB[SB];
+  if (T > 0) {
+    ld.template issue<false>(a, w, t_begin * kBN, kbuf[0]);
+    ld.template issue<true>(a, w, t_begin * kBN, vbuf[0]);
+    if (PIPE && T > 1) ld.template issue<false>(a, w, (t_begin + 1) * kBN, kbuf[1]);
+    lds_fill_barrier();
+    if constexpr (PIPE) compute_s(sA, kbuf[0]);
+    int i = 0;
+    for (; i + 2 < T; i += 2) {
+      step(NotLast{}, i, sA, sB);
+      step(NotLast{}, i + 1, sB, sA);
+    }
+    if (i + 1 < T) {
+      step(NotLast{}, i, sA, sB);
+      step(Last{}, i + 1, sB, sA);
+    } else {
+      step(Last{}, i, sA, sB);
+    }
+  }
+
+  const float l_tot = l_run + xor32(l_run);
+  if (S == 1) {
+    if (qrow < w.Lq) {
+      const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
+      const int64_t base = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + hi * 4;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t off = base + d * 32 + g * 8;
+          const float x0 = o[d][g * 4 + 0] * inv, x1 = o[d][g * 4 + 1] * inv;
+          const float x2 = o[d][g * 4 + 2] * inv, x3 = o[d][g * 4 + 3] * inv;
+          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
+              (u32x2){pack2<BF>(x0, x1), pack2<BF>(x2, x3)};
+        }
+      }
+    }
+  } else {
+    const int64_t slot = static_cast<int64_t>(split) * gridDim.x + blockIdx.x;
+    const int r = wave * kWaveRows + l32;
+    if (hi == 0) {
+      float* ml = a.part_ml + (slot * kBM + r) * 2;
+      ml[0] = m_run;
+      ml[1] = l_tot;
+    }
+    float* po = a.part_o + (slot * kBM + r) * D + hi * 4;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
+            (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
+  }
+}
+
+}  // namespace fa2

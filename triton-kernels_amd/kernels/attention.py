@@ -189,7 +189,7 @@ def flash_attention_v2(
     p.kv_heads = kv_heads
     p.head_dim = head_dim
     p.q_len = M
-    p.kv_len = N if layout != _fa2.LAYOUT_PAGED else 0
+    p.kv_len = N if layout != _fa2.LAYOUT_PAGED else total_cache
     p.q_sb, p.q_sh, p.q_ss = _strides(q)
     p.k_sb, p.k_sh, p.k_ss = _strides(k)
     p.v_sb, p.v_sh, p.v_ss = _strides(v)
