@@ -82,6 +82,7 @@ struct KArgs {
   int32_t batch, hq, hkv, q_len, kv_len, page_size;
   int32_t nqb;          // dense/paged: q-blocks per sequence
   int32_t work_ub;      // ragged/paged: capacity of the work list
+  int32_t npairs;       // work_ub * hkv: (item, kv head) pairs the grid covers
   int32_t mask;         // enum fa2_mask
   int32_t num_splits;   // >= 1
   float scale_log2;     // softmax_scale * log2(e)
@@ -201,14 +202,29 @@ struct Work {
   int off;                 // causal diagonal offset: key j visible iff j <= i + off
 };
 
+// Workgroup ids are dispatched round-robin over the 8 XCDs (each with its own
+// L2).  Ids are laid out as ((blk * G + g) * 8 + p): the 8 (item, kv head)
+// pairs of block `blk` go to 8 different XCDs, and the G query heads that
+// share one kv head land on the same XCD at ids 8 apart, so their K/V tiles
+// are fetched into one L2.  Items (and so LPT order) ascend with blk.
+constexpr int kXcds = 8;
+
 template <int MODE>
 __device__ __forceinline__ Work decode_work(const KArgs& a, int L) {
   Work w;
   w.valid = true;
-  w.h = L % a.hq;
-  const int item = L / a.hq;
   const int group = a.hq / a.hkv;
-  w.kvh = w.h / group;  // == h * Hkv / Hq (attention.py:463)
+  const int p = L % kXcds;
+  const int rest = L / kXcds;
+  const int g = rest % group;
+  const int pair = (rest / group) * kXcds + p;
+  if (pair >= a.npairs) {
+    w.valid = false;
+    return w;
+  }
+  const int item = pair / a.hkv;
+  w.kvh = pair % a.hkv;
+  w.h = w.kvh * group + g;  // kv head = h * Hkv / Hq (attention.py:463)
   if constexpr (MODE == FA2_LAYOUT_DENSE) {
     const int rank = item / a.batch;
     w.b = item % a.batch;

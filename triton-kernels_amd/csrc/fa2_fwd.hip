@@ -48,7 +48,8 @@ bool stride_ok(int64_t s, int eb) { return ((s * eb) & 15) == 0; }
 // capacity of the ragged/paged work list.
 struct Plan {
   int64_t work_ub;  // (sequence, q-block) slots
-  int64_t grid_x;   // work_ub * Hq
+  int64_t npairs;   // work_ub * Hkv
+  int64_t grid_x;   // npairs rounded up to kXcds, times Hq / Hkv
   int splits;
   bool buf;         // K/V byte offsets fit the 31-bit buffer-load path
   uint32_t pool_bytes_k, pool_bytes_v;
@@ -111,8 +112,11 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     pl->work_ub = nqb + p->batch;  // sum_b ceil(Lq_b/BM) <= ceil(Tq/BM) + B
   else
     pl->work_ub = nqb * p->batch;
-  pl->grid_x = pl->work_ub * p->q_heads;
-  if (pl->grid_x > INT32_MAX || pl->work_ub > INT32_MAX) return FA2_ERR_TOO_LARGE;
+  // (item, kv head) pairs rounded up to whole blocks of kXcds pairs, each
+  // pair expanded to its Hq/Hkv query heads (decode_work)
+  pl->npairs = pl->work_ub * p->kv_heads;
+  pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds * (p->q_heads / p->kv_heads);
+  if (pl->grid_x > INT32_MAX || pl->npairs > INT32_MAX) return FA2_ERR_TOO_LARGE;
 
   int splits = p->num_splits;
   if (splits == 0) {
@@ -124,8 +128,9 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     if (p->layout == FA2_LAYOUT_PAGED) kv_ub = INT32_MAX;  // lengths live on the device
     const int64_t tiles = cdiv(kv_ub, kBN);
     splits = 1;
-    if (pl->grid_x > 0 && pl->grid_x < slots) {
-      int64_t s = cdiv(slots, pl->grid_x);
+    const int64_t units = pl->npairs * (p->q_heads / p->kv_heads);  // real workgroups
+    if (units > 0 && units < slots) {
+      int64_t s = cdiv(slots, units);
       const int64_t by_tiles = tiles / 4;
       if (s > by_tiles) s = by_tiles;
       if (s > FA2_MAX_SPLITS) s = FA2_MAX_SPLITS;
@@ -273,6 +278,7 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
   a.page_size = static_cast<int32_t>(p->page_size > 0 ? p->page_size : 1);
   a.nqb = static_cast<int32_t>(cdiv(p->q_len, kBM));
   a.work_ub = static_cast<int32_t>(pl.work_ub);
+  a.npairs = static_cast<int32_t>(pl.npairs);
   a.mask = p->mask;
   a.num_splits = pl.splits;
   a.scale_log2 = p->softmax_scale * 1.4426950408889634f;

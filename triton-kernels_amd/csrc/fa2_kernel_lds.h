@@ -288,6 +288,8 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         ld.template issue<false>(a, w, k0 + (PIPE ? 2 : 1) * kBN, kbuf[(PIPE ? i : i + 1) & 1]);
       ld.template issue<true>(a, w, k0 + kBN, vbuf[(i + 1) & 1]);
     }
+    // scores of tile i must exist before they are masked
+    if constexpr (!PIPE) compute_s(s_cur, kbuf[i & 1]);
     if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
@@ -299,7 +301,6 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         }
       }
     }
-    if constexpr (!PIPE) compute_s(s_cur, kbuf[i & 1]);
     if constexpr (!kLast && PIPE) compute_s(s_nxt, kbuf[(i + 1) & 1]);
 
     float mx = -INFINITY;
