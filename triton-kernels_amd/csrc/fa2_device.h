@@ -182,6 +182,18 @@ __device__ __forceinline__ f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// acc + x.lo + x.hi for a packed pair of 16-bit values (v_dot2 with (1, 1))
+template <bool BF>
+__device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
+  if constexpr (BF) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x),
+                                           (bf16x2){(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+  } else {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x),
+                                  (f16x2){(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+  }
+}
+
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

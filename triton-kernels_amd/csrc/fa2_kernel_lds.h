@@ -265,7 +265,10 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
 
   const DirectLoader<D, MODE, BUF, DT> ld(a, tid);
 
+  // MFMA phases run at raised wave priority: when the other wave on the SIMD
+  // is in its softmax (VALU) phase, the MFMA issue is not starved.
   auto compute_s = [&](f32x16 (&s)[SB], const char* kb) {
+    __builtin_amdgcn_s_setprio(1);
     const lds_char_t* kl = to_lds(const_cast<char*>(kb));
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
@@ -277,6 +280,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         s[sb] = mma32<BF>(kf, qf[cc], s[sb]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   auto step = [&](auto last, int i, f32x16 (&s_cur)[SB], f32x16 (&s_nxt)[SB]) {
@@ -291,13 +295,16 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     // scores of tile i must exist before they are masked
     if constexpr (!PIPE) compute_s(s_cur, kbuf[i & 1]);
     if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
+      // key = k0 + 4*hi + c with c a compile-time offset per accumulator:
+      // visible iff c <= lim (sequence end and, if causal, the diagonal)
+      int lim = w.Lk - 1 - k0 - hi * 4;
+      if (causal) lim = min(lim, qrow + w.off - k0 - hi * 4);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
         for (int i2 = 0; i2 < 16; ++i2) {
-          const int key = k0 + sb * 32 + (i2 >> 2) * 8 + hi * 4 + (i2 & 3);
-          const bool ok = (key < w.Lk) && (!causal || key <= qrow + w.off);
-          if (!ok) s_cur[sb][i2] = -INFINITY;
+          const int c = sb * 32 + (i2 >> 2) * 8 + (i2 & 3);
+          if (c > lim) s_cur[sb][i2] = -INFINITY;
         }
       }
     }
@@ -315,16 +322,13 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     const float m_new = need ? mt : m_run;
     m_run = m_new;
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    float rs = 0.f;
     u32x4 pf[kBN / 16];
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
       float p[16];
 #pragma unroll
-      for (int i2 = 0; i2 < 16; ++i2) {
+      for (int i2 = 0; i2 < 16; ++i2)
         p[i2] = fast_exp2(__builtin_fmaf(s_cur[sb][i2], a.scale_log2, -m_use));
-        rs += p[i2];
-      }
 #pragma unroll
       for (int half = 0; half < 2; ++half)
         pf[sb * 2 + half] = (u32x4){pack2<BF>(p[half * 8 + 0], p[half * 8 + 1]),
@@ -332,6 +336,13 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
                                     pack2<BF>(p[half * 8 + 4], p[half * 8 + 5]),
                                     pack2<BF>(p[half * 8 + 6], p[half * 8 + 7])};
     }
+    // row sum of the rounded P, i.e. of exactly the weights the PV MFMA
+    // applies: one v_dot2 (x . (1,1) + acc, fp32 accumulate) per packed pair
+    float rs = 0.f;
+#pragma unroll
+    for (int c = 0; c < kBN / 16; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rs = dot2_ones<BF>(pf[c][j], rs);
     l_run = l_run * alpha + rs;
     if (__any(need)) {
 #pragma unroll
@@ -339,6 +350,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     }
     // O^T += V^T P^T; V^T fragments from two transposed reads per MFMA
     const lds_char_t* vl = to_lds(vbuf[i & 1]);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
       const uint32_t voff = voff0 ^ (64u * d);
@@ -353,6 +365,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         o[d] = mma32<BF>((u32x4){l2[0], l2[1], h2[0], h2[1]}, pf[c], o[d]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if constexpr (!kLast) lds_fill_barrier();
   };
   using NotLast = std::integral_constant<bool, false>;
