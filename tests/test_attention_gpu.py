@@ -201,6 +201,37 @@ def test_layout_equivalence_on_gpu():
         assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("key", [0, 5, 37, 63, 64, 100, 190])
+def test_dominant_key_selects_its_value(D, dtype, key):
+    """All probability mass on one key: the output row is that key's V row.
+    Each key sits in one lane half of the score fragment, so a wrong
+    cross-lane max/sum exchange shows up as a factor-of-two error here."""
+    g = torch.Generator().manual_seed(key)
+    B, H, L = 1, 4, 200
+    u = torch.randn(H, D, generator=g)
+    u = u / u.norm(dim=-1, keepdim=True)
+    q = (8.0 * u)[None, :, None, :].expand(B, H, 96, D).contiguous()
+    k = 0.05 * torch.randn(B, H, L, D, generator=g)
+    k[:, :, key] = 4.0 * (D ** 0.5) * u
+    v = torch.randn(B, H, L, D, generator=g)
+    out = fa2()(q.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV)).float().cpu()
+    want = v[:, :, key:key + 1, :].to(dtype).float().expand_as(out)
+    torch.testing.assert_close(out, want, atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_constant_v_gives_constant_rows(layout):
+    case = make_case(3, 8, 2, 128, "self", torch.bfloat16, layout, 1200)
+    row = (torch.arange(128) % 7 - 3).to(torch.bfloat16)
+    for v in case.vs:
+        v[:] = row
+    outs, _ = run_case(case, layout, True)
+    for o in outs:
+        assert torch.equal(o.float(), row.float().expand_as(o))
+
+
 def test_non_contiguous_inputs():
     """[B,S,H,D] storage viewed as [B,H,S,D] (last dim still contiguous)."""
     g = torch.Generator().manual_seed(5)

@@ -194,7 +194,12 @@ __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
   }
 }
 
-__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+// Reductions over the lane pair (l, l ^ 32) through ds_bpermute.
+// (v_permlane32_swap would avoid the LDS crossbar, but this compiler folds
+// __builtin_amdgcn_permlane32_swap(x, x) into one result register used for
+// both halves, which silently breaks the reduction.)
+__device__ __forceinline__ float max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
+__device__ __forceinline__ float sum_xor32(float x) { return x + __shfl_xor(x, 32, 64); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
@@ -574,7 +579,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
     for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
       for (int i2 = 0; i2 < 16; ++i2) mx = fmaxf(mx, s_cur[sb][i2]);
-    mx = fmaxf(mx, xor32(mx));
+    mx = max_xor32(mx);
     const float mt = mx * a.scale_log2;
     const bool need = mt > m_run + kRescaleThreshold;
     const float alpha = need ? fast_exp2(m_run - mt) : 1.0f;
@@ -635,7 +640,12 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
       ld.commit_k(ks_base + L::kKTile);
     }
     __syncthreads();
-    if constexpr (PIPE) compute_s(sA, 0);
+    if constexpr (PIPE) {
+      compute_s(sA, 0);
+      // step 0 rewrites K buffer 0 with K(t0+2): all waves must be done
+      // reading K(t0) first
+      __syncthreads();
+    }
     int i = 0;
     for (; i + 2 < T; i += 2) {
       step(NotLast{}, i, sA, sB);
@@ -649,7 +659,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
     }
   }
 
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = sum_xor32(l_run);
   if (S == 1) {
     if (qrow < w.Lq) {
       const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference

@@ -181,15 +181,17 @@ __device__ __forceinline__ void lds_fill_barrier() {
 #ifndef FA2_LDS_OCCUPANCY
 #define FA2_LDS_OCCUPANCY 2
 #endif
-// PIPE: K runs two tiles ahead and the S MFMAs of tile t+1 overlap the
-// softmax of tile t; otherwise K runs one tile ahead and S(t) starts step t.
-// Measured on MI355X (bf16, D=128): the pipelined form needs more than the
-// 256 VGPRs of two waves per SIMD and spills; the plain form is faster
-// (c2 669 vs 614 TFLOP/s) while D=64 pipelines without spilling.
+// PIPE: K runs two tiles ahead and the S MFMAs of tile t+1 are interleaved
+// (sched_group_barrier, FA2_SGB VALU instructions per MFMA) with the softmax
+// of tile t in one basic block; otherwise K runs one tile ahead and S(t)
+// starts step t.  Measured on MI355X, bf16 D=128 (same run): c2 625 -> 675,
+// c5 960 -> 1010 TFLOP/s for plain -> pipelined+interleaved.
 #ifndef FA2_LDS_PIPE
-#define FA2_LDS_PIPE_DEFAULT(D) ((D) <= 64)
-#else
+#define FA2_LDS_PIPE 1
+#endif
 #define FA2_LDS_PIPE_DEFAULT(D) (FA2_LDS_PIPE != 0)
+#ifndef FA2_SGB
+#define FA2_SGB 7
 #endif
 template <int DT, int D, int MODE, bool BUF, bool PIPE = FA2_LDS_PIPE_DEFAULT(D)>
 __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kernel(KArgs a) {
@@ -265,10 +267,9 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
 
   const DirectLoader<D, MODE, BUF, DT> ld(a, tid);
 
-  // MFMA phases run at raised wave priority: when the other wave on the SIMD
-  // is in its softmax (VALU) phase, the MFMA issue is not starved.
+  // (no s_setprio here: it would end the scheduling region and undo the
+  // interleaving of these MFMAs with the softmax)
   auto compute_s = [&](f32x16 (&s)[SB], const char* kb) {
-    __builtin_amdgcn_s_setprio(1);
     const lds_char_t* kl = to_lds(const_cast<char*>(kb));
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
@@ -280,7 +281,6 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         s[sb] = mma32<BF>(kf, qf[cc], s[sb]);
       }
     }
-    __builtin_amdgcn_s_setprio(0);
   };
 
   auto step = [&](auto last, int i, f32x16 (&s_cur)[SB], f32x16 (&s_nxt)[SB]) {
@@ -315,10 +315,11 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
       for (int i2 = 0; i2 < 16; ++i2) mx = fmaxf(mx, s_cur[sb][i2]);
-    mx = fmaxf(mx, xor32(mx));
+    mx = max_xor32(mx);
     const float mt = mx * a.scale_log2;
     const bool need = mt > m_run + kRescaleThreshold;
-    const float alpha = need ? fast_exp2(m_run - mt) : 1.0f;
+    // branch-free (exp2(0) = 1) so the whole softmax stays one basic block
+    const float alpha = fast_exp2(need ? (m_run - mt) : 0.0f);
     const float m_new = need ? mt : m_run;
     m_run = m_new;
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
@@ -344,7 +345,22 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
 #pragma unroll
       for (int j = 0; j < 4; ++j) rs = dot2_ones<BF>(pf[c][j], rs);
     l_run = l_run * alpha + rs;
-    if (__any(need)) {
+#if FA2_SGB > 0
+    // interleave the S(t+1) MFMAs (and their K reads) with the softmax VALU
+    // work of tile t inside this basic block: 1 LDS read, 1 MFMA, N VALU
+    if constexpr (PIPE && !kLast) {
+#pragma unroll
+      for (int k = 0; k < SB * DC; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, FA2_SGB, 0);
+      }
+    }
+#endif
+    // The rescale branch is rarely taken; tying its condition to the row sum
+    // (never -1) keeps the compiler from hoisting it above the exps, which
+    // would split the MFMA/softmax block in two.
+    if (__any(need) && rs != -1.0f) {
 #pragma unroll
       for (int d = 0; d < DB; ++d) o[d] *= alpha;
     }
@@ -377,7 +393,12 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     ld.template issue<true>(a, w, t_begin * kBN, vbuf[0]);
     if (PIPE && T > 1) ld.template issue<false>(a, w, (t_begin + 1) * kBN, kbuf[1]);
     lds_fill_barrier();
-    if constexpr (PIPE) compute_s(sA, kbuf[0]);
+    if constexpr (PIPE) {
+      compute_s(sA, kbuf[0]);
+      // step 0 refills kbuf[0] with K(t0+2): every wave must have finished
+      // reading K(t0) first (the barrier also waits for the LDS reads)
+      __syncthreads();
+    }
     int i = 0;
     for (; i + 2 < T; i += 2) {
       step(NotLast{}, i, sA, sB);
@@ -391,7 +412,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     }
   }
 
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = sum_xor32(l_run);
   if (S == 1) {
     if (qrow < w.Lq) {
       const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
