@@ -80,6 +80,7 @@ struct KArgs {
   int64_t o_sb, o_sh, o_ss;
   int64_t k_table_stride, v_table_stride;
   int32_t batch, hq, hkv, q_len, kv_len, page_size;
+  int32_t page_shift;   // log2(page_size) if a power of two, else -1
   int32_t nqb;          // dense/paged: q-blocks per sequence
   int32_t work_ub;      // ragged/paged: capacity of the work list
   int32_t npairs;       // work_ub * hkv: (item, kv head) pairs the grid covers

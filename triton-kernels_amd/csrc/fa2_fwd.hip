@@ -276,6 +276,9 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
   a.q_len = static_cast<int32_t>(p->q_len);
   a.kv_len = static_cast<int32_t>(p->kv_len);
   a.page_size = static_cast<int32_t>(p->page_size > 0 ? p->page_size : 1);
+  a.page_shift = -1;
+  for (int s = 0; s < 31; ++s)
+    if ((int64_t(1) << s) == a.page_size) a.page_shift = s;
   a.nqb = static_cast<int32_t>(cdiv(p->q_len, kBM));
   a.work_ub = static_cast<int32_t>(pl.work_ub);
   a.npairs = static_cast<int32_t>(pl.npairs);

@@ -50,14 +50,17 @@ __device__ __forceinline__ lds_char_t* to_lds(void* p) {
 // behind it (it cannot tell the double-buffer halves apart).  Completion is
 // awaited explicitly by lds_fill_barrier() before the buffer is read; the
 // waits the compiler emits for its own loads only get more conservative
-// (vector-memory loads retire in order).
+// (vector-memory loads retire in order).  No "memory" clobber: the target
+// buffer is not read before the next barrier (volatile asm is not moved
+// across it), the source K/V is never written, and without the clobber the
+// block-table reads stay eligible for the scalar unit.
 __device__ __forceinline__ void dma_buffer_x4(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "buffer_load_dwordx4 %1, %2, 0 offen lds"
       :
       : "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))), "v"(voff), "s"(rsrc)
-      : "memory", "m0");
+      : "m0");
 }
 
 __device__ __forceinline__ void dma_global_x4(const void* gptr, uint32_t lds_addr) {
@@ -66,7 +69,21 @@ __device__ __forceinline__ void dma_global_x4(const void* gptr, uint32_t lds_add
       "global_load_lds_dwordx4 %1, off"
       :
       : "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))), "v"(gptr)
-      : "memory", "m0");
+      : "m0");
+}
+
+// One 32-bit read of read-only global memory at a wave-uniform address through
+// the scalar unit (the block table is written before the kernel starts; the
+// scalar cache is invalidated at launch).
+__device__ __forceinline__ int scalar_load_i32(const int32_t* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a)));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
+  const uint64_t sa = (static_cast<uint64_t>(hi) << 32) | lo;
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(sa));
+  return v;
 }
 
 // Buffer descriptor as four SGPR words (base, stride 0, num_records, flags).
@@ -101,19 +118,43 @@ struct DirectLoader {
   }
   __device__ __forceinline__ int slot_of() const { return lane % G::kNC; }
 
+  // tile rows covered by one wave instruction, and this lane's row among them
+  static constexpr int kRPI = 64 / G::kNC;
+  __device__ __forceinline__ int lane_row() const { return lane / G::kNC; }
+
   __device__ __forceinline__ DirectLoader(const KArgs& a, int tid) {
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     lane = tid & 63;
-    if constexpr (MODE != FA2_LAYOUT_PAGED) {
-      const uint32_t krs = static_cast<uint32_t>(a.k_ss * kEB);
-      const uint32_t vrs = static_cast<uint32_t>(a.v_ss * kEB);
+    const uint32_t krs = static_cast<uint32_t>(a.k_ss * kEB);
+    const uint32_t vrs = static_cast<uint32_t>(a.v_ss * kEB);
 #pragma unroll
-      for (int j = 0; j < kInstr; ++j) {
-        const int r = row_of(j);
-        kvo[j] = r * krs + ((slot_of() ^ G::k(r)) * 16);
-        vvo[j] = r * vrs + ((slot_of() ^ G::v(r)) * 16);
-      }
+    for (int j = 0; j < kInstr; ++j) {
+      const int r = row_of(j);
+      // dense/ragged: offset from the tile's first row; paged: from the first
+      // row of this instruction's kRPI-row group (its page row is added later)
+      const int rr = (MODE == FA2_LAYOUT_PAGED) ? lane_row() : r;
+      kvo[j] = rr * krs + ((slot_of() ^ G::k(r)) * 16);
+      vvo[j] = rr * vrs + ((slot_of() ^ G::v(r)) * 16);
     }
+  }
+
+  // Physical row of logical row n0 (uniform across the wave) and whether the
+  // kRPI rows n0.. share its page (page_size a multiple of kRPI): then one
+  // scalar table read serves the whole instruction.
+  __device__ __forceinline__ static int paged_row_uniform(const KArgs& a, const int32_t* table,
+                                                          int64_t tstride, int b, int n) {
+    int pidx, poff;
+    if (a.page_shift >= 0) {
+      pidx = n >> a.page_shift;
+      poff = n & (a.page_size - 1);
+    } else {
+      pidx = n / a.page_size;
+      poff = n - pidx * a.page_size;
+    }
+    // The index is wave-uniform: read the entry with a scalar load (SMEM,
+    // counted by lgkmcnt, so it never waits behind the K/V DMAs in vmcnt).
+    const int idx = __builtin_amdgcn_readfirstlane(static_cast<int>(b * tstride + pidx));
+    return scalar_load_i32(table + idx) * a.page_size + poff;
   }
 
   __device__ __forceinline__ static int paged_row(const int32_t* table, int64_t tstride, int b,
@@ -136,14 +177,28 @@ struct DirectLoader {
                                       IS_V ? a.pool_bytes_v : a.pool_bytes_k);
         const int32_t* tbl = IS_V ? a.v_table : a.k_table;
         const int64_t ts = IS_V ? a.v_table_stride : a.k_table_stride;
+        if (a.page_size % kRPI == 0) {
 #pragma unroll
-        for (int j = 0; j < kInstr; ++j) {
-          const int r = row_of(j);
-          const int n = k0 + r;
-          const int nc = min(n, w.Lk - 1);
-          const uint32_t prow = static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
-          const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
-          dma_buffer_x4(rsrc, ldst + j * 1024, n < w.Lk ? prow * rsb + col : 0xFFFFFF00u);
+          for (int j = 0; j < kInstr; ++j) {
+            const int n0 = k0 + (wave * kInstr + j) * kRPI;  // uniform
+            const int n0c = min(n0, w.Lk - 1);
+            const uint32_t urow =
+                static_cast<uint32_t>(paged_row_uniform(a, tbl, ts, w.b, n0c));
+            const uint32_t off = urow * rsb + (IS_V ? vvo[j] : kvo[j]);
+            dma_buffer_x4(rsrc, ldst + j * 1024,
+                          n0 + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < kInstr; ++j) {
+            const int r = row_of(j);
+            const int n = k0 + r;
+            const int nc = min(n, w.Lk - 1);
+            const uint32_t prow =
+                static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
+            const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
+            dma_buffer_x4(rsrc, ldst + j * 1024, n < w.Lk ? prow * rsb + col : 0xFFFFFF00u);
+          }
         }
       } else {
         const uint32_t lim = static_cast<uint32_t>(w.Lk - k0) * rsb;
