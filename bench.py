@@ -116,7 +116,20 @@ def main(argv=None):
     ap.add_argument("--flush", action="store_true",
                     help="write 512 MiB between steps (outside the events) to flush L2/MALL")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 times) to calibrate "
+                         "the FETCH_SIZE / WRITE_SIZE counters against known bytes")
     args = ap.parse_args(argv)
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the flash_attention_v2 hot path has no "

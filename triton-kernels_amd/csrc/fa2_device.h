@@ -59,6 +59,11 @@ constexpr int kBN = 64;        // keys per KV tile
 constexpr int kCostBuckets = 4096;
 constexpr int kPlanThreads = 1024;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: P <= 2^8 between rescales
+// LDS operand reads are issued this many MFMAs ahead of their MFMA
+#ifndef FA2_READ_AHEAD
+#define FA2_READ_AHEAD 4
+#endif
+constexpr int kReadAhead = FA2_READ_AHEAD;
 // buffer descriptor word 3 for gfx9-family raw (stride 0) buffers, 32-bit data format
 constexpr int kBufferFlags = 0x00020000;
 

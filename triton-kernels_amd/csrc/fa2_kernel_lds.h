@@ -401,14 +401,19 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
       for (int j = 0; j < 4; ++j) rs = dot2_ones<BF>(pf[c][j], rs);
     l_run = l_run * alpha + rs;
 #if FA2_SGB > 0
-    // interleave the S(t+1) MFMAs (and their K reads) with the softmax VALU
-    // work of tile t inside this basic block: 1 LDS read, 1 MFMA, N VALU
+    // Interleave the S(t+1) MFMAs with the softmax VALU work of tile t inside
+    // this basic block, with the K fragment reads running kReadAhead MFMAs
+    // ahead so that no MFMA waits on a just-issued LDS read:
+    //   R x kReadAhead, then per MFMA: 1 MFMA, N VALU, 1 R (for MFMA k + ahead)
     if constexpr (PIPE && !kLast) {
+      constexpr int kN = SB * DC;
+      constexpr int kAhead = kReadAhead < kN ? kReadAhead : kN;
+      __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
 #pragma unroll
-      for (int k = 0; k < SB * DC; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int k = 0; k < kN; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, FA2_SGB, 0);
+        if (k + kAhead < kN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
 #endif
@@ -421,7 +426,6 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     }
     // O^T += V^T P^T; V^T fragments from two transposed reads per MFMA
     const lds_char_t* vl = to_lds(vbuf[i & 1]);
-    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
       const uint32_t voff = voff0 ^ (64u * d);
@@ -436,7 +440,19 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         o[d] = mma32<BF>((u32x4){l2[0], l2[1], h2[0], h2[1]}, pf[c], o[d]);
       }
     }
-    __builtin_amdgcn_s_setprio(0);
+#if FA2_SGB > 0
+    {
+      // V reads run kReadAhead MFMAs ahead of the PV MFMAs (2 reads each)
+      constexpr int kN = DB * (kBN / 16);
+      constexpr int kAhead = kReadAhead < kN ? kReadAhead : kN;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kAhead, 1);
+#pragma unroll
+      for (int k = 0; k < kN; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        if (k + kAhead < kN) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      }
+    }
+#endif
     if constexpr (!kLast) lds_fill_barrier();
   };
   using NotLast = std::integral_constant<bool, false>;

@@ -178,46 +178,87 @@ def flash_attention_v2(
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
     dev = q.device
-    p = _fa2.Fa2Params()
-    p.layout = layout
-    p.dtype = _DTYPES[q.dtype]
-    p.mask = (_fa2.MASK_NONE if not is_causal else
-              (_fa2.MASK_TOP_LEFT if causal_alignment == "top_left" else _fa2.MASK_BOTTOM_RIGHT))
-    p.num_splits = int(num_splits)
-    p.batch = batch
-    p.q_heads = q_heads
-    p.kv_heads = kv_heads
-    p.head_dim = head_dim
-    p.q_len = M
-    p.kv_len = N if layout != _fa2.LAYOUT_PAGED else total_cache
-    p.q_sb, p.q_sh, p.q_ss = _strides(q)
-    p.k_sb, p.k_sh, p.k_ss = _strides(k)
-    p.v_sb, p.v_sh, p.v_ss = _strides(v)
-    p.o_sb, p.o_sh, p.o_ss = _strides(out)
-    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
-    keep = []
+    mask = (_fa2.MASK_NONE if not is_causal else
+            (_fa2.MASK_TOP_LEFT if causal_alignment == "top_left" else _fa2.MASK_BOTTOM_RIGHT))
+    qi = kvi = kt = vt = None
     if layout == _fa2.LAYOUT_RAGGED:
         qi = _index_tensor(q_indptr, dev)
         kvi = _index_tensor(kv_indptr, dev)
-        keep += [qi, kvi]
-        p.q_indptr, p.kv_indptr = qi.data_ptr(), kvi.data_ptr()
     elif layout == _fa2.LAYOUT_PAGED:
         kvi = _index_tensor(kv_indptr, dev)
         kt = _table(k_block_table, dev)
         vt = _table(v_block_table, dev)
-        keep += [kvi, kt, vt]
-        p.kv_indptr, p.k_block_table, p.v_block_table = kvi.data_ptr(), kt.data_ptr(), vt.data_ptr()
-        p.k_table_stride, p.v_table_stride = kt.stride(0), vt.stride(0)
-        p.page_size = int(kv_page_size)
-    p.softmax_scale = head_dim ** -0.5
 
-    with torch.cuda.device(dev):
-        ws_bytes = _fa2.workspace_size(p)
+    # Everything but the pointers depends only on the call signature: build
+    # that part of the parameter block (and its workspace size) once.
+    key = (layout, q.dtype, mask, int(num_splits), dev.index, q.shape, q.stride(), k.shape,
+           k.stride(), v.stride(), out.stride(), batch,
+           None if kt is None else (kt.stride(0), vt.stride(0), int(kv_page_size)))
+    cached = _PLAN_CACHE.get(key)
+    if cached is None:
+        p = _fa2.Fa2Params()
+        p.layout = layout
+        p.dtype = _DTYPES[q.dtype]
+        p.mask = mask
+        p.num_splits = int(num_splits)
+        p.batch = batch
+        p.q_heads = q_heads
+        p.kv_heads = kv_heads
+        p.head_dim = head_dim
+        p.q_len = M
+        p.kv_len = N if layout != _fa2.LAYOUT_PAGED else total_cache
+        p.q_sb, p.q_sh, p.q_ss = _strides(q)
+        p.k_sb, p.k_sh, p.k_ss = _strides(k)
+        p.v_sb, p.v_sh, p.v_ss = _strides(v)
+        p.o_sb, p.o_sh, p.o_ss = _strides(out)
+        if kt is not None:
+            p.k_table_stride, p.v_table_stride = kt.stride(0), vt.stride(0)
+            p.page_size = int(kv_page_size)
+        p.softmax_scale = head_dim ** -0.5
+        # validation needs the layout's pointers; they are overwritten per call
+        p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+        if qi is not None:
+            p.q_indptr = qi.data_ptr()
+        if kvi is not None:
+            p.kv_indptr = kvi.data_ptr()
+        if kt is not None:
+            p.k_block_table, p.v_block_table = kt.data_ptr(), vt.data_ptr()
+        with torch.cuda.device(dev):
+            ws_bytes = _fa2.workspace_size(p)
+        cached = (bytes(p), ws_bytes)
+        if len(_PLAN_CACHE) >= _PLAN_CACHE_MAX:
+            _PLAN_CACHE.clear()
+        _PLAN_CACHE[key] = cached
+
+    p = _fa2.Fa2Params.from_buffer_copy(cached[0])
+    ws_bytes = cached[1]
+    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    if qi is not None:
+        p.q_indptr = qi.data_ptr()
+    if kvi is not None:
+        p.kv_indptr = kvi.data_ptr()
+    if kt is not None:
+        p.k_block_table, p.v_block_table = kt.data_ptr(), vt.data_ptr()
+
+    switch = dev.index != torch.cuda.current_device()
+    if switch:
+        prev = torch.cuda.current_device()
+        torch.cuda.set_device(dev)
+    try:
+        stream = torch.cuda.current_stream(dev)
         ws = None
         if ws_bytes:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
-        _fa2.forward(p, torch.cuda.current_stream(dev).cuda_stream)
+        _fa2.forward(p, stream.cuda_stream)
         if ws is not None:
-            ws.record_stream(torch.cuda.current_stream(dev))
+            ws.record_stream(stream)
+    finally:
+        if switch:
+            torch.cuda.set_device(prev)
     return out
+
+
+# call signature -> (static bytes of the parameter block, workspace bytes)
+_PLAN_CACHE: dict = {}
+_PLAN_CACHE_MAX = 4096
