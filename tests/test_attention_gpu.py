@@ -201,24 +201,46 @@ def test_layout_equivalence_on_gpu():
         assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize("hkv", [4, 1])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("key", [0, 5, 37, 63, 64, 100, 190])
-def test_dominant_key_selects_its_value(D, dtype, key):
+def test_dominant_key_selects_its_value(D, dtype, key, hkv):
     """All probability mass on one key: the output row is that key's V row.
     Each key sits in one lane half of the score fragment, so a wrong
-    cross-lane max/sum exchange shows up as a factor-of-two error here."""
+    cross-lane max/sum exchange shows up as a factor-of-two error here.
+    hkv=1 shares one K/V head among the 4 query heads (two-head kernel)."""
     g = torch.Generator().manual_seed(key)
     B, H, L = 1, 4, 200
-    u = torch.randn(H, D, generator=g)
+    u = torch.randn(hkv, D, generator=g)
     u = u / u.norm(dim=-1, keepdim=True)
-    q = (8.0 * u)[None, :, None, :].expand(B, H, 96, D).contiguous()
-    k = 0.05 * torch.randn(B, H, L, D, generator=g)
+    q = (8.0 * u).repeat_interleave(H // hkv, 0)[None, :, None, :].expand(B, H, 96, D)
+    q = q.contiguous()
+    k = 0.05 * torch.randn(B, hkv, L, D, generator=g)
     k[:, :, key] = 4.0 * (D ** 0.5) * u
-    v = torch.randn(B, H, L, D, generator=g)
+    v = torch.randn(B, hkv, L, D, generator=g)
     out = fa2()(q.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV)).float().cpu()
-    want = v[:, :, key:key + 1, :].to(dtype).float().expand_as(out)
-    torch.testing.assert_close(out, want, atol=2e-2, rtol=2e-2)
+    want = v[:, :, key:key + 1, :].to(dtype).float().repeat_interleave(H // hkv, 1)
+    torch.testing.assert_close(out, want.expand_as(out), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("group", [2, 4, 3])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_grouped_equals_expanded_heads(layout, D, group, splits):
+    """Grouped heads (two query heads per workgroup) and the same problem with
+    K/V repeated per query head (one head per workgroup) run the same
+    per-row arithmetic over the same tiles: the outputs are identical."""
+    case = make_case(3, 2 * group, 2, D, "self", torch.bfloat16, layout, 1300 + group,
+                     q_range=(30, 400), dense_q_range=(300, 300))
+    q, k, v, kw = pack(case, layout, device=DEV, shuffled_pages=True, seed=1)
+    out = fa2()(q, k, v, is_causal=True, num_splits=splits, **kw)
+    ke = k.repeat_interleave(group, dim=1)  # the head dim of every k/v layout
+    ve = v.repeat_interleave(group, dim=1)
+    ref = fa2()(q, ke, ve, is_causal=True, num_splits=splits, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), ref.cpu())
 
 
 @pytest.mark.parametrize("layout", LAYOUTS)

@@ -91,6 +91,7 @@ struct KArgs {
   int32_t npairs;       // work_ub * hkv: (item, kv head) pairs the grid covers
   int32_t mask;         // enum fa2_mask
   int32_t num_splits;   // >= 1
+  int32_t part_slots;   // split partials: slots per split (one per (item, head) unit)
   float scale_log2;     // softmax_scale * log2(e)
   uint32_t pool_bytes_k;  // paged + buffer path: bytes of the k cache from the kv-head 0 row 0
   uint32_t pool_bytes_v;
@@ -201,11 +202,23 @@ __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
 }
 
 // Reductions over the lane pair (l, l ^ 32) through ds_bpermute.
-// (v_permlane32_swap would avoid the LDS crossbar, but this compiler folds
-// __builtin_amdgcn_permlane32_swap(x, x) into one result register used for
-// both halves, which silently breaks the reduction.)
 __device__ __forceinline__ float max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
 __device__ __forceinline__ float sum_xor32(float x) { return x + __shfl_xor(x, 32, 64); }
+
+// The same maximum on the VALU (v_permlane32_swap, gfx950), for code that runs
+// while other waves saturate the LDS pipeline, which ds_bpermute also uses.
+// swap(a, b) exchanges the upper half of a with the lower half of b, so with
+// a = b = x the two results hold x[l & 31] and x[32 + (l & 31)] in every lane.
+// Both results pass through integer variables and an empty asm: this
+// compiler otherwise rewrites bit_cast<float>(result[1]) into result[0],
+// which silently turns the reduction into the identity.
+__device__ __forceinline__ float max_xor32_valu(float x) {
+  const unsigned xb = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(xb, xb, false, false);
+  unsigned lo = r[0], up = r[1];
+  asm volatile("" : "+v"(lo), "+v"(up));
+  return fmaxf(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, up));
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
@@ -218,6 +231,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 struct Work {
   bool valid;
   int b, h, kvh, qblk;
+  int pair;                // (item, kv head) pair index
+  int hg;                  // h - kvh * (Hq / Hkv): head index within the kv group
   int Lq, Lk;
   int64_t q_base, o_base;  // element offset of row 0 of this (sequence, head)
   int64_t k_base, v_base;  // dense/ragged: row 0 of this (sequence, kv head);
@@ -232,22 +247,27 @@ struct Work {
 // are fetched into one L2.  Items (and so LPT order) ascend with blk.
 constexpr int kXcds = 8;
 
+// A unit may cover `heads` consecutive query heads of one kv group (the
+// ping-pong kernel takes two); w.h is then the first of them.
 template <int MODE>
-__device__ __forceinline__ Work decode_work(const KArgs& a, int L) {
+__device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1) {
   Work w;
   w.valid = true;
   const int group = a.hq / a.hkv;
+  const int units = (group + heads - 1) / heads;
   const int p = L % kXcds;
   const int rest = L / kXcds;
-  const int g = rest % group;
-  const int pair = (rest / group) * kXcds + p;
+  const int g = rest % units;
+  const int pair = (rest / units) * kXcds + p;
   if (pair >= a.npairs) {
     w.valid = false;
     return w;
   }
+  w.pair = pair;
   const int item = pair / a.hkv;
   w.kvh = pair % a.hkv;
-  w.h = w.kvh * group + g;  // kv head = h * Hkv / Hq (attention.py:463)
+  w.hg = g * heads;
+  w.h = w.kvh * group + w.hg;  // kv head = h * Hkv / Hq (attention.py:463)
   if constexpr (MODE == FA2_LAYOUT_DENSE) {
     const int rank = item / a.batch;
     w.b = item % a.batch;
@@ -537,12 +557,14 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
   // S^T block for the tile held in K buffer `kb`.
   auto compute_s = [&](f32x16 (&s)[SB], int kb) {
     const uint16_t* ks = ks_base + kb * L::kKTile;
+    // accumulators interleaved (c-major): back-to-back dependent MFMAs stall
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-      s[sb] = (f32x16){};
-      const uint16_t* krow = ks + (sb * 32 + l32) * L::kKStride + hi * 8;
+    for (int sb = 0; sb < SB; ++sb) s[sb] = (f32x16){};
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
+    for (int c = 0; c < DC; ++c) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+        const uint16_t* krow = ks + (sb * 32 + l32) * L::kKStride + hi * 8;
         const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + c * 16);
         s[sb] = mma32<BF>(kf, qf[c], s[sb]);
       }
@@ -618,10 +640,10 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
     // O^T += V^T P^T
     const uint16_t* vt = vt_base + (i & 1) * L::kVTile;
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      const uint16_t* vrow = vt + (d * 32 + l32) * L::kVStride + hi * 8;
+    for (int c = 0; c < kBN / 16; ++c) {
 #pragma unroll
-      for (int c = 0; c < kBN / 16; ++c) {
+      for (int d = 0; d < DB; ++d) {
+        const uint16_t* vrow = vt + (d * 32 + l32) * L::kVStride + hi * 8;
         const u32x4 vf = *reinterpret_cast<const u32x4*>(vrow + c * 16);
         o[d] = mma32<BF>(vf, pf[c], o[d]);
       }
@@ -688,7 +710,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
     }
   } else {
     // Split partials: slot (split, workgroup), row r of the q-block.
-    const int64_t slot = static_cast<int64_t>(split) * gridDim.x + blockIdx.x;
+    const int64_t slot = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = wave * kWaveRows + l32;
     if (hi == 0) {
       float* ml = a.part_ml + (slot * kBM + r) * 2;
@@ -717,7 +739,7 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   constexpr int kTPR = D / 4;  // threads per row, 4 floats each
   constexpr int kRowsPerPass = kThreads / kTPR;
   const int S = a.num_splits;
-  const int G = gridDim.x;
+  const int G = a.part_slots;
   const int col = (threadIdx.x % kTPR) * 4;
   for (int r = threadIdx.x / kTPR; r < kBM; r += kRowsPerPass) {
     const int qrow = q0 + r;

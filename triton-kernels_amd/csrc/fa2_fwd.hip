@@ -16,6 +16,13 @@
 
 #include "fa2_device.h"
 #include "fa2_kernel_lds.h"
+#include "fa2_kernel_pp.h"
+
+// 1: fp16/bf16 with an even number of query heads per kv head run the
+// two-head ping-pong kernel; 0: always the one-head kernel.
+#ifndef FA2_PP
+#define FA2_PP 1
+#endif
 
 namespace fa2 {
 namespace {
@@ -50,6 +57,8 @@ struct Plan {
   int64_t work_ub;  // (sequence, q-block) slots
   int64_t npairs;   // work_ub * Hkv
   int64_t grid_x;   // npairs rounded up to kXcds, times Hq / Hkv
+  bool pp;          // two-head ping-pong kernel
+  int64_t grid_pp;  // its grid: npairs rounded up to kXcds, times Hq / Hkv / 2
   int splits;
   bool buf;         // K/V byte offsets fit the 31-bit buffer-load path
   uint32_t pool_bytes_k, pool_bytes_v;
@@ -115,8 +124,11 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   // (item, kv head) pairs rounded up to whole blocks of kXcds pairs, each
   // pair expanded to its Hq/Hkv query heads (decode_work)
   pl->npairs = pl->work_ub * p->kv_heads;
-  pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds * (p->q_heads / p->kv_heads);
+  const int64_t group = p->q_heads / p->kv_heads;
+  pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds * group;
   if (pl->grid_x > INT32_MAX || pl->npairs > INT32_MAX) return FA2_ERR_TOO_LARGE;
+  pl->pp = FA2_PP && p->dtype != FA2_DTYPE_F32 && group % 2 == 0;
+  pl->grid_pp = cdiv(pl->npairs, kXcds) * kXcds * cdiv(group, 2);
 
   int splits = p->num_splits;
   if (splits == 0) {
@@ -170,6 +182,13 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
       hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
     else
       hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st, a);
+  } else if (pl.pp) {
+    const dim3 gpp(pl.grid_pp, pl.splits);
+    if (pl.buf)
+      hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true>), gpp, dim3(kPPThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, false>), gpp, dim3(kPPThreads), 0, st,
+                         a);
   } else {
     if (pl.buf)
       hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
@@ -284,6 +303,7 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
   a.npairs = static_cast<int32_t>(pl.npairs);
   a.mask = p->mask;
   a.num_splits = pl.splits;
+  a.part_slots = static_cast<int32_t>(pl.grid_x);
   a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
   a.pool_bytes_k = pl.pool_bytes_k;
   a.pool_bytes_v = pl.pool_bytes_v;

@@ -100,11 +100,13 @@ __device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(const_cast<void*>(p))));
 }
 
-template <int D, int MODE, bool BUF, int DT>
+// Tile loads shared by NW waves (each issues kInstr 1 KiB instructions).
+template <int D, int MODE, bool BUF, int DT, int NW = kWaves>
 struct DirectLoader {
   using G = SwzGeo<D>;
   static constexpr int kEB = 2;
-  static constexpr int kInstr = G::kNC / 4;  // 1 KiB wave instructions per tensor per tile
+  static constexpr int kInstr = G::kNC / NW;  // 1 KiB wave instructions per tensor per tile
+  static_assert(kInstr * NW == G::kNC, "tile must split evenly over the loading waves");
   static_assert(kInstr >= 1, "head dim");
 
   // dense/ragged: byte offset (row * stride + swizzled chunk) of this lane's
@@ -122,9 +124,13 @@ struct DirectLoader {
   static constexpr int kRPI = 64 / G::kNC;
   __device__ __forceinline__ int lane_row() const { return lane / G::kNC; }
 
-  __device__ __forceinline__ DirectLoader(const KArgs& a, int tid) {
-    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    lane = tid & 63;
+  __device__ __forceinline__ DirectLoader(const KArgs& a, int tid)
+      : DirectLoader(a, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63) {}
+
+  // wv: index of this wave among the NW loading waves
+  __device__ __forceinline__ DirectLoader(const KArgs& a, int wv, int ln) {
+    wave = wv;
+    lane = ln;
     const uint32_t krs = static_cast<uint32_t>(a.k_ss * kEB);
     const uint32_t vrs = static_cast<uint32_t>(a.v_ss * kEB);
 #pragma unroll
@@ -326,11 +332,13 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
   // interleaving of these MFMAs with the softmax)
   auto compute_s = [&](f32x16 (&s)[SB], const char* kb) {
     const lds_char_t* kl = to_lds(const_cast<char*>(kb));
+    // accumulators interleaved (cc-major): back-to-back dependent MFMAs stall
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-      s[sb] = (f32x16){};
+    for (int sb = 0; sb < SB; ++sb) s[sb] = (f32x16){};
 #pragma unroll
-      for (int cc = 0; cc < DC; ++cc) {
+    for (int cc = 0; cc < DC; ++cc) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
         const u32x4 kf =
             *(const lds_u32x4_t*)(kl + sb * 32 * G::kRowBytes + (koff0 ^ (32u * cc)));
         s[sb] = mma32<BF>(kf, qf[cc], s[sb]);
@@ -427,10 +435,10 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     // O^T += V^T P^T; V^T fragments from two transposed reads per MFMA
     const lds_char_t* vl = to_lds(vbuf[i & 1]);
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      const uint32_t voff = voff0 ^ (64u * d);
+    for (int c = 0; c < kBN / 16; ++c) {
 #pragma unroll
-      for (int c = 0; c < kBN / 16; ++c) {
+      for (int d = 0; d < DB; ++d) {
+        const uint32_t voff = voff0 ^ (64u * d);
         const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (lds_v4i16_t*)(vl + (16 * c) * G::kRowBytes + voff));
         const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -501,7 +509,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
       }
     }
   } else {
-    const int64_t slot = static_cast<int64_t>(split) * gridDim.x + blockIdx.x;
+    const int64_t slot = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = wave * kWaveRows + l32;
     if (hi == 0) {
       float* ml = a.part_ml + (slot * kBM + r) * 2;
