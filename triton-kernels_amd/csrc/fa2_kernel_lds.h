@@ -233,6 +233,51 @@ struct DirectLoader {
   }
 };
 
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2_t;
+
+// Output rows go out through LDS: in the O^T accumulator a lane holds 4
+// dims of one row per register group, so direct stores write 8-byte pieces
+// of 32 different rows per instruction.  Each wave instead writes its 32 x D
+// tile (normalised, rounded) into its own LDS region and reads it back as
+// whole rows: every global store then covers 16-byte chunks of complete rows.
+template <int D>
+struct OStage {
+  static constexpr int kStride = D * 2 + 16;  // row pitch; the pad spreads banks
+  static constexpr int kBytes = kWaveRows * kStride;
+};
+
+// o: this wave's O^T accumulators (row l32, dims 32d + 8g + 4hi + j at
+// o[d][4g + j]); inv: 1 / row sum of this lane's row; stage: the wave's
+// region of OStage<D>::kBytes; rows row0.. of the output at `base`, only
+// rows < Lq are stored.
+template <int DT, int D>
+__device__ __forceinline__ void store_o_staged(const f32x16 (&o)[D / 32], float inv, char* stage,
+                                               void* out, int64_t base, int64_t o_ss, int row0,
+                                               int Lq, int lane) {
+  constexpr bool BF = Elt<DT>::kBF;
+  constexpr int kS = OStage<D>::kStride;
+  constexpr int kChunks = D / 8;              // 16-byte chunks per row
+  constexpr int kRowsPerRead = 64 / kChunks;  // rows covered by one wave read
+  const int l32 = lane & 31, hi = lane >> 5;
+  lds_char_t* st = to_lds(stage);
+#pragma unroll
+  for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *(lds_u32x2_t*)(st + l32 * kS + (d * 32 + g * 8 + hi * 4) * 2) =
+          (u32x2){pack2<BF>(o[d][g * 4 + 0] * inv, o[d][g * 4 + 1] * inv),
+                  pack2<BF>(o[d][g * 4 + 2] * inv, o[d][g * 4 + 3] * inv)};
+  const int ch = lane % kChunks;
+#pragma unroll
+  for (int it = 0; it < kWaveRows / kRowsPerRead; ++it) {
+    const int r = it * kRowsPerRead + lane / kChunks;
+    const u32x4 v = *(const lds_u32x4_t*)(st + r * kS + ch * 16);
+    if (row0 + r < Lq)
+      *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + base +
+                                static_cast<int64_t>(row0 + r) * o_ss + ch * 8) = v;
+  }
+}
+
 // Wait for this wave's outstanding direct-to-LDS loads (vmcnt), then barrier.
 __device__ __forceinline__ void lds_fill_barrier() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -493,21 +538,11 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
 
   const float l_tot = sum_xor32(l_run);
   if (S == 1) {
-    if (qrow < w.Lq) {
-      const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
-      const int64_t base = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + hi * 4;
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t off = base + d * 32 + g * 8;
-          const float x0 = o[d][g * 4 + 0] * inv, x1 = o[d][g * 4 + 1] * inv;
-          const float x2 = o[d][g * 4 + 2] * inv, x3 = o[d][g * 4 + 3] * inv;
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
-              (u32x2){pack2<BF>(x0, x1), pack2<BF>(x2, x3)};
-        }
-      }
-    }
+    static_assert(kWaves * OStage<D>::kBytes <= sizeof(lds), "O staging exceeds LDS");
+    __syncthreads();  // the last tile's buffers may still be read by other waves
+    const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
+    store_o_staged<DT, D>(o, inv, lds + wave * OStage<D>::kBytes, a.o, w.o_base, a.o_ss,
+                          wq_first, w.Lq, lane);
   } else {
     const int64_t slot = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = wave * kWaveRows + l32;

@@ -338,26 +338,17 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
     pp_barrier();
     phase_m(Y{}, N{}, T);
     if (grp == 0) pp_barrier();  // pairs with group 1's last barrier
+    // every wave is past its last LDS read: the whole LDS is free
+    if (S == 1) pp_barrier();
   }
 
   if (!hok) return;
   const float l_tot = sum_xor32(l_run);
   if (S == 1) {
-    if (qrow < w.Lq) {
-      const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
-      const int64_t base = o_base + static_cast<int64_t>(qrow) * a.o_ss + hi * 4;
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t off = base + d * 32 + g * 8;
-          const float x0 = o[d][g * 4 + 0] * inv, x1 = o[d][g * 4 + 1] * inv;
-          const float x2 = o[d][g * 4 + 2] * inv, x3 = o[d][g * 4 + 3] * inv;
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
-              (u32x2){pack2<BF>(x0, x1), pack2<BF>(x2, x3)};
-        }
-      }
-    }
+    static_assert(kPPWaves * OStage<D>::kBytes <= sizeof(lds), "O staging exceeds LDS");
+    const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
+    store_o_staged<DT, D>(o, inv, lds + wave * OStage<D>::kBytes, a.o, o_base, a.o_ss, wq_first,
+                          w.Lq, lane);
   } else {
     // partials go to the slot the one-head-per-unit layout gives this head
     // (decode_work with heads = 1), which the combine kernel reads
