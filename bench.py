@@ -6,10 +6,13 @@ configuration BASELINE.json's metric is quoted on.  A "step" is one
 resident in HBM.  Prints ONE JSON line (rank 0, N=1):
 
   value       algorithmic TFLOP/s of the whole step (host wall clock over K
-              steps, bracketed by torch.cuda.synchronize());
-  roofline    achieved TFLOP/s of the forward kernel from HIP events recorded
-              around every step on the stream the kernels run on, against
-              the dense bf16/fp16 MFMA peak (256 CU x 4096 FLOP/clk x 2.4 GHz);
+              back-to-back steps, bracketed by torch.cuda.synchronize());
+  roofline    achieved TFLOP/s per launch from one pair of HIP events around
+              the K back-to-back steps on the stream the kernels run on,
+              against the dense bf16/fp16 MFMA peak (256 CU x 4096 FLOP/clk x
+              2.4 GHz); `traffic` = HBM bytes per launch from the committed
+              rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the same workload
+              (profiles/hbm_traffic.json), null if there is none;
   cpu_baseline  the reference test suite's oracle (fp32 SDPA per sequence,
               oracle.sdpa_reference) on the host CPU, on a bounded sample.
 
@@ -104,6 +107,25 @@ def cpu_baseline(w: W.Workload, budget_s: float = 20.0):
     }
 
 
+def hbm_traffic(config: str, dtype: str):
+    """HBM bytes per launch of the workload's forward kernel, from the
+    committed counter summary (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE,
+    KiB per dispatch, each scaled by the factor the same counter shows for a
+    plain device copy of known size); None when not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    e = table.get("workloads", {}).get(f"{config}_{dtype}")
+    if not e:
+        return None
+    sc = table["copy_calibration"]
+    return int(round((e["fetch_kib"] * sc["fetch_scale"] + e["write_kib"] * sc["write_scale"])
+                     * 1024))
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,24 +183,32 @@ def main(argv=None):
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        if flush_buf is not None:
+    if flush_buf is None:
+        # back-to-back steps; one event pair on the kernels' stream
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        kern_avg = start.elapsed_time(stop) / args.steps
+        ms_per_step = wall * 1e3 / args.steps
+    else:
+        # cold caches: a flush between steps, each step between its own events
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        for i in range(args.steps):
             flush_buf.fill_(i & 0xFF)
-        ev[i][0].record(stream)
-        step()
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
-    kern_avg = sum(kern_ms) / len(kern_ms)
-    kern_med = sorted(kern_ms)[len(kern_ms) // 2]
-    ms_per_step = wall * 1e3 / args.steps
-    if flush_buf is not None:
-        ms_per_step = kern_avg  # wall clock includes the flush writes
+            ev[i][0].record(stream)
+            step()
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+        kern_avg = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+        ms_per_step = kern_avg  # wall clock would include the flush writes
     value = fl / (ms_per_step * 1e-3) / 1e12
     achieved = fl / (kern_avg * 1e-3) / 1e12
     bound = "mfma" if fl / nbytes > (PEAK_TFLOPS * 1e12) / (PEAK_HBM_GBS * 1e9) else "hbm"
@@ -213,9 +243,8 @@ def main(argv=None):
             "peak": round(PEAK_TFLOPS, 1),
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": hbm_traffic(args.config, DTYPE_NAME[w.dtype]),
             "kernel_ms_avg": round(kern_avg, 5),
-            "kernel_ms_median": round(kern_med, 5),
             "hbm_gbs_algorithmic": round(nbytes / (kern_avg * 1e-3) / 1e9, 1),
         },
         "cpu_baseline": None,
