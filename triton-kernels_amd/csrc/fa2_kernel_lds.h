@@ -122,6 +122,8 @@ struct DirectLoader {
 
   // tile rows covered by one wave instruction, and this lane's row among them
   static constexpr int kRPI = 64 / G::kNC;
+  // consecutive tile rows covered by one wave's kInstr instructions
+  static constexpr int kSpan = kInstr * kRPI;
   __device__ __forceinline__ int lane_row() const { return lane / G::kNC; }
 
   __device__ __forceinline__ DirectLoader(const KArgs& a, int tid)
@@ -183,7 +185,19 @@ struct DirectLoader {
                                       IS_V ? a.pool_bytes_v : a.pool_bytes_k);
         const int32_t* tbl = IS_V ? a.v_table : a.k_table;
         const int64_t ts = IS_V ? a.v_table_stride : a.k_table_stride;
-        if (a.page_size % kRPI == 0) {
+        if (a.page_size % kSpan == 0) {
+          // the wave's kSpan rows (starting at a multiple of kSpan) lie in
+          // one page: one table read for all its instructions
+          const int n0 = k0 + wave * kSpan;  // uniform
+          const uint32_t urow =
+              static_cast<uint32_t>(paged_row_uniform(a, tbl, ts, w.b, min(n0, w.Lk - 1)));
+#pragma unroll
+          for (int j = 0; j < kInstr; ++j) {
+            const uint32_t off = (urow + j * kRPI) * rsb + (IS_V ? vvo[j] : kvo[j]);
+            dma_buffer_x4(rsrc, ldst + j * 1024,
+                          n0 + j * kRPI + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+          }
+        } else if (a.page_size % kRPI == 0) {
 #pragma unroll
           for (int j = 0; j < kInstr; ++j) {
             const int n0 = k0 + (wave * kInstr + j) * kRPI;  // uniform
