@@ -92,6 +92,7 @@ struct KArgs {
   int32_t mask;         // enum fa2_mask
   int32_t num_splits;   // >= 1
   int32_t part_slots;   // split partials: slots per split (one per (item, head) unit)
+  int32_t units;        // two-head kernel: units its persistent grid walks
   float scale_log2;     // softmax_scale * log2(e)
   uint32_t pool_bytes_k;  // paged + buffer path: bytes of the k cache from the kv-head 0 row 0
   uint32_t pool_bytes_v;
@@ -210,8 +211,9 @@ __device__ __forceinline__ float sum_xor32(float x) { return x + __shfl_xor(x, 3
 // swap(a, b) exchanges the upper half of a with the lower half of b, so with
 // a = b = x the two results hold x[l & 31] and x[32 + (l & 31)] in every lane.
 // Both results pass through integer variables and an empty asm: this
-// compiler otherwise rewrites bit_cast<float>(result[1]) into result[0],
-// which silently turns the reduction into the identity.
+// compiler reads element 0 when bit_cast is applied to a subscripted vector
+// element (bit_cast<float>(result[1]) becomes result[0]), which silently
+// turns the reduction into the identity.
 __device__ __forceinline__ float max_xor32_valu(float x) {
   const unsigned xb = __builtin_bit_cast(unsigned, x);
   const auto r = __builtin_amdgcn_permlane32_swap(xb, xb, false, false);

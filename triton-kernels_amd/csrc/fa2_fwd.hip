@@ -23,6 +23,10 @@
 #ifndef FA2_PP
 #define FA2_PP 1
 #endif
+// 1: the two-head kernel runs one workgroup per CU over all units
+#ifndef FA2_PP_PERSISTENT
+#define FA2_PP_PERSISTENT 1
+#endif
 
 namespace fa2 {
 namespace {
@@ -183,7 +187,13 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
     else
       hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st, a);
   } else if (pl.pp) {
-    const dim3 gpp(pl.grid_pp, pl.splits);
+    // persistent: one workgroup per CU walks the units (when not split)
+    int64_t wgs = pl.grid_pp;
+    if (pl.splits == 1 && FA2_PP_PERSISTENT) {
+      const int64_t cus = cu_count_current_device();
+      if (wgs > cus) wgs = cus;
+    }
+    const dim3 gpp(static_cast<uint32_t>(wgs), pl.splits);
     if (pl.buf)
       hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true>), gpp, dim3(kPPThreads), 0, st, a);
     else
@@ -304,6 +314,7 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
   a.mask = p->mask;
   a.num_splits = pl.splits;
   a.part_slots = static_cast<int32_t>(pl.grid_x);
+  a.units = static_cast<int32_t>(pl.grid_pp);
   a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
   a.pool_bytes_k = pl.pool_bytes_k;
   a.pool_bytes_v = pl.pool_bytes_v;

@@ -100,6 +100,12 @@ __device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(const_cast<void*>(p))));
 }
 
+// LDS pointer at byte address `addr` (an integer conversion: the LDS null
+// pointer is 0xFFFFFFFF, so offsets must not be added to a converted null).
+__device__ __forceinline__ lds_char_t* lds_ptr(uint32_t addr) {
+  return (lds_char_t*)(static_cast<uintptr_t>(addr));
+}
+
 // Tile loads shared by NW waves (each issues kInstr 1 KiB instructions).
 template <int D, int MODE, bool BUF, int DT, int NW = kWaves>
 struct DirectLoader {
@@ -289,6 +295,47 @@ __device__ __forceinline__ void store_o_staged(const f32x16 (&o)[D / 32], float 
     if (row0 + r < Lq)
       *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + base +
                                 static_cast<int64_t>(row0 + r) * o_ss + ch * 8) = v;
+  }
+}
+
+// The same through buffer stores in passes of DP dims (stage: OStage<DP>
+// bytes).  The descriptor `out` starts at row row0 of the tile and covers
+// only the rows < Lq, which the hardware range check enforces: every store
+// instruction is issued whatever the row count (a fixed vmcnt contribution
+// of kOStoreOps<D, DP> per lane).
+template <int D, int DP>
+constexpr int kOStoreOps = (D / DP) * (kWaveRows * DP / 512);
+
+template <int DT, int D, int DP>
+__device__ __forceinline__ void store_o_staged_buf(const f32x16 (&o)[D / 32], float inv,
+                                                   char* stage, __amdgpu_buffer_rsrc_t out,
+                                                   int64_t o_ss, int lane) {
+  static_assert(D % DP == 0 && DP % 32 == 0, "pass width");
+  constexpr bool BF = Elt<DT>::kBF;
+  constexpr int kS = OStage<DP>::kStride;
+  constexpr int kChunks = DP / 8;             // 16-byte chunks per staged row
+  constexpr int kRowsPerRead = 64 / kChunks;  // rows covered by one wave read
+  const int l32 = lane & 31, hi = lane >> 5;
+  const uint32_t rs = static_cast<uint32_t>(o_ss * 2);
+  lds_char_t* st = to_lds(stage);
+  const int ch = lane % kChunks;
+#pragma unroll
+  for (int p = 0; p < D / DP; ++p) {
+#pragma unroll
+    for (int dd = 0; dd < DP / 32; ++dd) {
+      const int d = p * (DP / 32) + dd;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(lds_u32x2_t*)(st + l32 * kS + (dd * 32 + g * 8 + hi * 4) * 2) =
+            (u32x2){pack2<BF>(o[d][g * 4 + 0] * inv, o[d][g * 4 + 1] * inv),
+                    pack2<BF>(o[d][g * 4 + 2] * inv, o[d][g * 4 + 3] * inv)};
+    }
+#pragma unroll
+    for (int it = 0; it < kWaveRows / kRowsPerRead; ++it) {
+      const int r = it * kRowsPerRead + lane / kChunks;
+      const u32x4 v = *(const lds_u32x4_t*)(st + r * kS + ch * 16);
+      __builtin_amdgcn_raw_buffer_store_b128(v, out, r * rs + (p * DP + ch * 8) * 2, 0, 0);
+    }
   }
 }
 

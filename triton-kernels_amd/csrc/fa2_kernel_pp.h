@@ -37,6 +37,16 @@
 
 namespace fa2 {
 
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 constexpr int kPPWaves = 8;
 constexpr int kPPThreads = kPPWaves * 64;
 constexpr int kPPSlots = 3;
@@ -74,6 +84,15 @@ __device__ __forceinline__ void pp_wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// One unit of work: a q-block of two query heads of one kv head (and one
+// split of its KV range).
+struct PPUnit {
+  Work w;
+  int T, t_begin, q0;
+  int64_t q_base, o_base;  // this group's head
+  bool hok;                // this group's head exists (odd head groups)
+};
+
 template <int DT, int D, int MODE, bool BUF>
 __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   static_assert(DT != FA2_DTYPE_F32, "fp32 uses the register-staged kernel");
@@ -85,8 +104,14 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   using LD = DirectLoader<D, MODE, BUF, DT, kWaves>;  // group 0 loads
   constexpr int kI = LD::kInstr;
   constexpr int kTile = G::kTileBytes;
+  constexpr int kSlotBytes = 2 * kPPSlots * kTile;
+  constexpr int kStageDims = 64;  // output staged in passes of 64 dims
+  constexpr int kStores = kOStoreOps<D, kStageDims>;
 
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kPPSlots * kTile];
+  // K/V slots, then one output staging region per wave (separate, so the
+  // next unit's tiles can land while this unit's rows are being stored)
+  __shared__ __attribute__((aligned(1024)))
+  char lds[kSlotBytes + kPPWaves * OStage<kStageDims>::kBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -95,38 +120,11 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   const int wq = wave & 3;
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-
-  const Work w = decode_work<MODE>(a, blockIdx.x, 2);
-  if (!w.valid) return;
   const int group = a.hq / a.hkv;
-  const bool hok = w.hg + grp < group;  // odd group: the second head may not exist
-  const int64_t q_base = w.q_base + grp * a.q_sh;
-  const int64_t o_base = w.o_base + grp * a.o_sh;
-  const int q0 = w.qblk * kBM;
   const int split = blockIdx.y;
   const int S = a.num_splits;
-
-  const int kv_end = kv_end_for_block(a.mask, q0, w.Lq, w.Lk, w.off);
-  const int ntiles = (kv_end + kBN - 1) / kBN;
-  const int t_begin = (ntiles * split) / S;
-  const int t_end = (ntiles * (split + 1)) / S;
-  const int T = t_end - t_begin;
-
-  const int qrow = q0 + wq * kWaveRows + l32;
-  u32x4 qf[DC];
-  {
-    const bool ok = hok && qrow < w.Lq;
-    const int64_t base = q_base + static_cast<int64_t>(qrow) * a.q_ss + hi * 8;
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      Raw8<DT> r;
-      if (ok)
-        load_raw8<DT>(r, a.q, base + c * 16);
-      else
-        zero_raw8<DT>(r);
-      qf[c] = to16<DT>(r);
-    }
-  }
+  const bool causal = a.mask != FA2_MASK_NONE;
+  char* const stage = lds + kSlotBytes + wave * OStage<kStageDims>::kBytes;
 
   // per-lane LDS offsets, as in fa2_fwd_lds_kernel
   const uint32_t koff0 = l32 * G::kRowBytes + ((hi ^ G::k(l32)) * 16);
@@ -137,41 +135,139 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
     const int dim = 16 * (g & 1) + 4 * (i & 3);
     voff0 = r * G::kRowBytes + (((dim >> 3) ^ G::v(r)) * 16) + (dim & 7) * 2;
   }
+  const LD ld(a, wq, lane);
+
+  // Persistent: gridDim.x workgroups walk the units (heaviest first) in
+  // rounds; odd rounds run backwards over blocks of kXcds workgroups, which
+  // pairs heavy with light units and keeps each unit on the XCD that the
+  // unit layout of decode_work intends.
+  const int P = gridDim.x;
+  auto unit_index = [&](int r) -> int {
+    const int wg = blockIdx.x;
+    int pos = wg;
+    if (r & 1) pos = (P % kXcds) ? (P - 1 - wg) : ((P / kXcds - 1 - wg / kXcds) * kXcds + wg % kXcds);
+    return r * P + pos;
+  };
+  auto make_unit = [&](int L, PPUnit& u) -> bool {
+    u.w = decode_work<MODE>(a, L, 2);
+    if (!u.w.valid) return false;
+    u.hok = u.w.hg + grp < group;
+    u.q_base = u.w.q_base + grp * a.q_sh;
+    u.o_base = u.w.o_base + grp * a.o_sh;
+    u.q0 = u.w.qblk * kBM;
+    const int kv_end = kv_end_for_block(a.mask, u.q0, u.w.Lq, u.w.Lk, u.w.off);
+    const int ntiles = (kv_end + kBN - 1) / kBN;
+    u.t_begin = (ntiles * split) / S;
+    u.T = (ntiles * (split + 1)) / S - u.t_begin;
+    return true;
+  };
+  // next valid unit at round >= r (uniform); false when none is left
+  auto next_unit = [&](int& r, PPUnit& u) -> bool {
+    for (;; ++r) {
+      const int L = unit_index(r);
+      if (L >= a.units) return false;
+      if (make_unit(L, u)) return true;
+    }
+  };
+
+  u32x4 qf[DC];
+  auto load_q = [&](const PPUnit& u) {
+    const int qrow = u.q0 + wq * kWaveRows + l32;
+    const bool ok = u.hok && qrow < u.w.Lq;
+    const int64_t base = u.q_base + static_cast<int64_t>(qrow) * a.q_ss + hi * 8;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      Raw8<DT> r;
+      if (ok)
+        load_raw8<DT>(r, a.q, base + c * 16);
+      else
+        zero_raw8<DT>(r);
+      qf[c] = to16<DT>(r);
+    }
+  };
 
   f32x16 o[DB];
-#pragma unroll
-  for (int d = 0; d < DB; ++d) o[d] = (f32x16){};
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  const int wq_first = q0 + wq * kWaveRows;
-  const bool causal = a.mask != FA2_MASK_NONE;
-
-  const LD ld(a, wq, lane);
-  auto kslot = [&](int i) { return lds + (i % kPPSlots) * kTile; };
-  auto vslot = [&](int i) { return lds + (kPPSlots + i % kPPSlots) * kTile; };
-
+  float m_run, l_run;
   f32x16 s[SB];
   u32x4 pf[kBN / 16];
 
-  // M phase: PV of the previous tile, then S of this one.
-  auto phase_m = [&](auto has_pv, auto has_s, int i) {
-    constexpr bool kPV = decltype(has_pv)::value;
-    constexpr bool kS = decltype(has_s)::value;
-    // a scheduling region of its own: nothing moves in or out
-    __builtin_amdgcn_sched_barrier(0);
+  // wait until at most n of this wave's vector memory operations are
+  // outstanding; n is one of the counts this kernel produces
+  auto wait_vm = [&](int n) {
+    if (n >= 2 * kI + kStores)
+      pp_wait_vm<2 * kI + kStores>();
+    else if (n >= kI + kStores)
+      pp_wait_vm<kI + kStores>();
+    else if (n >= kStores && kStores > 2 * kI)
+      pp_wait_vm<kStores>();
+    else if (n >= 2 * kI)
+      pp_wait_vm<2 * kI>();
+    else if (n >= kI)
+      pp_wait_vm<kI>();
+    else if (n >= DC)
+      pp_wait_vm<DC>();
+    else
+      pp_wait_vm<0>();
+  };
+  using Y = std::integral_constant<bool, true>;
+  using N = std::integral_constant<bool, false>;
+
+  int r = 0;
+  PPUnit cur;
+  if (!next_unit(r, cur)) return;
+  int gb = 0;          // tile i of the current unit is tile gb + i of this workgroup's stream
+  bool pre = false;    // the current unit's Q and first tiles were issued by the previous one
+  for (;;) {
+    const int T = cur.T;
+    const PPUnit& u = cur;
+    const Work& w = u.w;
+    // The next unit is looked up at this one's tail, so that only one unit
+    // is live during the tile loop (scalar registers).  Its Q and first
+    // tiles are prefetched during this unit's last phases when it has
+    // tiles and there is one split (the store count below is fixed then).
+    PPUnit nxt;
+    int rn = r + 1;
+    bool has_next = false, pre_next = false;
+
+    auto kslot = [&](int i) { return lds + ((gb + i) % kPPSlots) * kTile; };
+    auto vslot = [&](int i) { return lds + (kPPSlots + (gb + i) % kPPSlots) * kTile; };
+    const int qrow = u.q0 + wq * kWaveRows + l32;
+    const int wq_first = u.q0 + wq * kWaveRows;
+
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = (f32x16){};
+    m_run = -INFINITY;
+    l_run = 0.f;
+    if (!pre) load_q(u);
+
+    // M phase: PV of the previous tile, then S of this one.
+    auto phase_m = [&](auto has_pv, auto has_s, int i) {
+      constexpr bool kPV = decltype(has_pv)::value;
+      constexpr bool kS = decltype(has_s)::value;
+      // slot bases resolved before the scheduling region (scalar work that
+      // would otherwise sit between the reads the region is ordering)
+      const uint32_t vbase = kPV ? lds_addr_of(vslot(i - 1)) : 0u;
+      const uint32_t kbase = kS ? lds_addr_of(kslot(i)) : 0u;
+      // a scheduling region of its own: nothing moves in or out
+      __builtin_amdgcn_sched_barrier(0);
 #if FA2_PP_PRIO
-    __builtin_amdgcn_s_setprio(FA2_PP_PRIO);
+      __builtin_amdgcn_s_setprio(FA2_PP_PRIO);
 #endif
-    // Consecutive MFMAs go to different accumulators (c-major for PV,
-    // cc-major for S): an MFMA that depends on the one just issued waits for
-    // it to finish, which doubles the time per MFMA.  Each accumulator still
-    // sums in the same order.
-    if constexpr (kPV) {
-      const lds_char_t* vl = to_lds(vslot(i - 1));
-#pragma unroll
-      for (int c = 0; c < kBN / 16; ++c) {
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
+      // Fragment k: the PV fragments first (c-major: V^T from two transposed
+      // reads; consecutive MFMAs go to different accumulators), then the S
+      // fragments (cc-major: one K row chunk).  Each accumulator still sums
+      // in the same order.  The reads are written kAhead fragments ahead of
+      // their MFMA, so that order holds even where the scheduler keeps the
+      // source order.
+      constexpr int kNPV = kPV ? DB * (kBN / 16) : 0;
+      constexpr int kN = kNPV + (kS ? SB * DC : 0);
+      constexpr int kAhead = FA2_PP_AHEAD < kN ? FA2_PP_AHEAD : kN;
+      const lds_char_t* vl = lds_ptr(vbase);
+      const lds_char_t* kl = lds_ptr(kbase);
+      auto frag = [&](auto kc) -> u32x4 {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k < kNPV) {
+          constexpr int c = k / DB, d = k % DB;
           const uint32_t voff = voff0 ^ (64u * d);
           const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_v4i16_t*)(vl + (16 * c) * G::kRowBytes + voff));
@@ -179,194 +275,221 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
               (lds_v4i16_t*)(vl + (16 * c + 8) * G::kRowBytes + voff));
           const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
           const u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
-          o[d] = mma32<BF>((u32x4){l2[0], l2[1], h2[0], h2[1]}, pf[c], o[d]);
+          return (u32x4){l2[0], l2[1], h2[0], h2[1]};
+        } else {
+          constexpr int kk = k - kNPV, cc = kk / SB, sb = kk % SB;
+          return *(const lds_u32x4_t*)(kl + sb * 32 * G::kRowBytes + (koff0 ^ (32u * cc)));
         }
+      };
+      auto mma_k = [&](auto kc, const u32x4& f) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k < kNPV) {
+          constexpr int c = k / DB, d = k % DB;
+          o[d] = mma32<BF>(f, pf[c], o[d]);
+        } else {
+          constexpr int kk = k - kNPV, cc = kk / SB, sb = kk % SB;
+          s[sb] = mma32<BF>(f, qf[cc], s[sb]);
+        }
+      };
+      if constexpr (kS) {
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb) s[sb] = (f32x16){};
       }
-    }
-    if constexpr (kS) {
-      const lds_char_t* kl = to_lds(kslot(i));
+      u32x4 fr[kN];
+      static_for<kAhead>([&](auto kc) { fr[decltype(kc)::value] = frag(kc); });
+      static_for<kN>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        mma_k(kc, fr[k]);
+        if constexpr (k + kAhead < kN)
+          fr[k + kAhead] = frag(std::integral_constant<int, k + kAhead>{});
+      });
+      // the same order as scheduling groups (reads of the first kAhead
+      // fragments, then per MFMA k: the MFMA, the reads of fragment k + kAhead)
+      {
+        constexpr int kPre2 = kAhead < kNPV ? kAhead : kNPV;  // PV MFMAs among the first kAhead
+        constexpr int kB1 = kNPV > kAhead ? kNPV - kAhead : 0;  // MFMAs followed by 2 reads
+        if constexpr (kPre2 > 0) __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPre2, 0);
+        if constexpr (kAhead > kPre2) __builtin_amdgcn_sched_group_barrier(0x100, kAhead - kPre2, 0);
 #pragma unroll
-      for (int sb = 0; sb < SB; ++sb) s[sb] = (f32x16){};
+        for (int k = 0; k < kB1; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
 #pragma unroll
-      for (int cc = 0; cc < DC; ++cc) {
+        for (int k = kB1; k < kN - kAhead; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kAhead, 0);
+      }
+#if FA2_PP_PRIO
+      __builtin_amdgcn_s_setprio(0);
+#endif
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // V phase: online softmax of tile i (scores in s), P^T into pf.
+    auto phase_v = [&](int i) {
+      const int k0 = (u.t_begin + i) * kBN;
+      if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
+        int lim = w.Lk - 1 - k0 - hi * 4;
+        if (causal) lim = min(lim, qrow + w.off - k0 - hi * 4);
+        // key offset c is hidden iff lim - c < 0: the sign, spread over the
+        // word, selects -inf (bit select, no compare masks in scalar registers)
 #pragma unroll
         for (int sb = 0; sb < SB; ++sb) {
-          const u32x4 kf =
-              *(const lds_u32x4_t*)(kl + sb * 32 * G::kRowBytes + (koff0 ^ (32u * cc)));
-          s[sb] = mma32<BF>(kf, qf[cc], s[sb]);
+#pragma unroll
+          for (int i2 = 0; i2 < 16; ++i2) {
+            const int c = sb * 32 + (i2 >> 2) * 8 + (i2 & 3);
+            const uint32_t hide = static_cast<uint32_t>((lim - c) >> 31);
+            // (bit_cast through a scalar: this compiler reads element 0 when
+            // bit_cast is applied to a subscripted vector element)
+            const float x = s[sb][i2];
+            s[sb][i2] = __builtin_bit_cast(
+                float, (hide & 0xFF800000u) | (~hide & __builtin_bit_cast(uint32_t, x)));
+          }
         }
       }
-    }
-    // Order: the reads of the first kAhead MFMAs, then per MFMA k the MFMA
-    // and the reads of MFMA k + kAhead (2 transposed V reads for a PV MFMA,
-    // 1 K read for an S MFMA), so no MFMA waits on a just-issued read.
-    {
-      constexpr int kNPV = kPV ? DB * (kBN / 16) : 0;
-      constexpr int kN = kNPV + (kS ? SB * DC : 0);
-      constexpr int kAhead = FA2_PP_AHEAD < kN ? FA2_PP_AHEAD : kN;
-      constexpr int kPre2 = kAhead < kNPV ? kAhead : kNPV;  // PV MFMAs among the first kAhead
-      constexpr int kB1 = kNPV > kAhead ? kNPV - kAhead : 0;  // MFMAs followed by 2 reads
-      if constexpr (kPre2 > 0) __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPre2, 0);
-      if constexpr (kAhead > kPre2) __builtin_amdgcn_sched_group_barrier(0x100, kAhead - kPre2, 0);
+      float mx = -INFINITY;
 #pragma unroll
-      for (int k = 0; k < kB1; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
+      for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-      for (int k = kB1; k < kN - kAhead; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, kAhead, 0);
-    }
-#if FA2_PP_PRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // V phase: online softmax of tile i (scores in s), P^T into pf.
-  auto phase_v = [&](int i) {
-    const int k0 = (t_begin + i) * kBN;
-    if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
-      int lim = w.Lk - 1 - k0 - hi * 4;
-      if (causal) lim = min(lim, qrow + w.off - k0 - hi * 4);
+        for (int i2 = 0; i2 < 16; ++i2) mx = fmaxf(mx, s[sb][i2]);
+      mx = max_xor32_valu(mx);
+      const float mt = mx * a.scale_log2;
+      const bool need = mt > m_run + kRescaleThreshold;
+      const float alpha = fast_exp2(need ? (m_run - mt) : 0.0f);
+      const float m_new = need ? mt : m_run;
+      m_run = m_new;
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
+        float p[16];
 #pragma unroll
-        for (int i2 = 0; i2 < 16; ++i2) {
-          const int c = sb * 32 + (i2 >> 2) * 8 + (i2 & 3);
-          if (c > lim) s[sb][i2] = -INFINITY;
+        for (int i2 = 0; i2 < 16; ++i2)
+          p[i2] = fast_exp2(__builtin_fmaf(s[sb][i2], a.scale_log2, -m_use));
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+          pf[sb * 2 + half] = (u32x4){pack2<BF>(p[half * 8 + 0], p[half * 8 + 1]),
+                                      pack2<BF>(p[half * 8 + 2], p[half * 8 + 3]),
+                                      pack2<BF>(p[half * 8 + 4], p[half * 8 + 5]),
+                                      pack2<BF>(p[half * 8 + 6], p[half * 8 + 7])};
+      }
+      float rs = 0.f;
+#pragma unroll
+      for (int c = 0; c < kBN / 16; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rs = dot2_ones<BF>(pf[c][j], rs);
+      l_run = l_run * alpha + rs;
+      if (__any(need)) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) o[d] *= alpha;
+      }
+    };
+
+    // group 0: loads issued at the start of V(i); returns this wave's count
+    auto issue_iter = [&](int i) -> int {
+      int n = 0;
+      if (i + 1 < T) {
+        ld.template issue<true>(a, w, (u.t_begin + i + 1) * kBN, vslot(i + 1));
+        n += kI;
+      }
+      if (i + 2 < T) {
+        ld.template issue<false>(a, w, (u.t_begin + i + 2) * kBN, kslot(i + 2));
+        n += kI;
+      }
+      return n;
+    };
+    // group 0: the first tiles of unit v (K(0), K(1) if any, V(0)), whose
+    // tile 0 is tile g0 of the stream
+    auto issue_first = [&](const PPUnit& v, int g0) {
+      char* k0s = lds + (g0 % kPPSlots) * kTile;
+      char* k1s = lds + ((g0 + 1) % kPPSlots) * kTile;
+      char* v0s = lds + (kPPSlots + g0 % kPPSlots) * kTile;
+      ld.template issue<false>(a, v.w, v.t_begin * kBN, k0s);
+      if (v.T > 1) ld.template issue<false>(a, v.w, (v.t_begin + 1) * kBN, k1s);
+      ld.template issue<true>(a, v.w, v.t_begin * kBN, v0s);
+    };
+
+    if (T > 0) {
+      if (grp == 0) {
+        if (!pre) issue_first(u, gb);
+        // K(0) (and Q) have landed: what was issued after K(0) may be in
+        // flight (K(1), V(0), and the previous unit's output stores)
+        wait_vm((T > 1 ? 2 * kI : kI) + (pre ? kStores : 0));
+      }
+      pp_barrier();
+      if (grp != 0) pp_barrier();  // group 1 runs one phase behind
+      phase_m(N{}, Y{}, 0);
+      pp_barrier();
+      for (int i = 0; i + 1 < T; ++i) {
+        int n = 0;
+        if (grp == 0) n = issue_iter(i);
+        phase_v(i);
+        // K(i+1) and V(i) (read from M(i+1) on) have landed; the loads of
+        // the current issue may still be in flight
+        if (grp == 0) wait_vm(n);
+        pp_barrier();
+        phase_m(Y{}, Y{}, i + 1);
+        pp_barrier();
+      }
+      has_next = next_unit(rn, nxt);
+      pre_next = has_next && nxt.T > 0 && S == 1;
+      // Q of the next unit: this group's last S is done
+      if (pre_next) load_q(nxt);
+      phase_v(T - 1);
+      // V(T-1), read by the last PV, has landed (the next Q may be in flight)
+      if (grp == 0) {
+        if (pre_next)
+          pp_wait_vm<DC>();
+        else
+          pp_wait_vm<0>();
+      }
+      pp_barrier();
+      // the first tiles of the next unit go to slots no longer read
+      if (pre_next && grp == 0) issue_first(nxt, gb + T);
+      phase_m(Y{}, N{}, T);
+      if (grp == 0) pp_barrier();  // pairs with group 1's last barrier
+    } else {
+      has_next = next_unit(rn, nxt);
+    }
+
+    if (u.hok) {
+      const float l_tot = sum_xor32(l_run);
+      if (S == 1) {
+        const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
+        const int nrows = max(0, min(w.Lq - wq_first, kWaveRows));
+        const __amdgpu_buffer_rsrc_t out = make_rsrc(
+            static_cast<uint16_t*>(a.o) + u.o_base + static_cast<int64_t>(wq_first) * a.o_ss,
+            static_cast<uint32_t>(nrows) * static_cast<uint32_t>(a.o_ss * 2));
+        store_o_staged_buf<DT, D, kStageDims>(o, inv, stage, out, a.o_ss, lane);
+      } else {
+        // partials go to the slot the one-head-per-unit layout gives this
+        // head (decode_work with heads = 1), which the combine kernel reads
+        const int unit =
+            ((w.pair / kXcds) * group + w.hg + grp) * kXcds + w.pair % kXcds;
+        const int64_t slot = static_cast<int64_t>(split) * a.part_slots + unit;
+        const int rr = wq * kWaveRows + l32;
+        if (hi == 0) {
+          float* ml = a.part_ml + (slot * kBM + rr) * 2;
+          ml[0] = m_run;
+          ml[1] = l_tot;
         }
+        float* po = a.part_o + (slot * kBM + rr) * D + hi * 4;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
+                (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
       }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-      for (int i2 = 0; i2 < 16; ++i2) mx = fmaxf(mx, s[sb][i2]);
-    mx = max_xor32_valu(mx);
-    const float mt = mx * a.scale_log2;
-    const bool need = mt > m_run + kRescaleThreshold;
-    const float alpha = fast_exp2(need ? (m_run - mt) : 0.0f);
-    const float m_new = need ? mt : m_run;
-    m_run = m_new;
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-#pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-      float p[16];
-#pragma unroll
-      for (int i2 = 0; i2 < 16; ++i2)
-        p[i2] = fast_exp2(__builtin_fmaf(s[sb][i2], a.scale_log2, -m_use));
-#pragma unroll
-      for (int half = 0; half < 2; ++half)
-        pf[sb * 2 + half] = (u32x4){pack2<BF>(p[half * 8 + 0], p[half * 8 + 1]),
-                                    pack2<BF>(p[half * 8 + 2], p[half * 8 + 3]),
-                                    pack2<BF>(p[half * 8 + 4], p[half * 8 + 5]),
-                                    pack2<BF>(p[half * 8 + 6], p[half * 8 + 7])};
-    }
-    float rs = 0.f;
-#pragma unroll
-    for (int c = 0; c < kBN / 16; ++c)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) rs = dot2_ones<BF>(pf[c][j], rs);
-    l_run = l_run * alpha + rs;
-    if (__any(need)) {
-#pragma unroll
-      for (int d = 0; d < DB; ++d) o[d] *= alpha;
-    }
-  };
 
-  // group 0: loads issued at the start of V(i); returns this wave's count
-  auto issue_iter = [&](int i) -> int {
-    int n = 0;
-    if (i + 1 < T) {
-      ld.template issue<true>(a, w, (t_begin + i + 1) * kBN, vslot(i + 1));
-      n += kI;
-    }
-    if (i + 2 < T) {
-      ld.template issue<false>(a, w, (t_begin + i + 2) * kBN, kslot(i + 2));
-      n += kI;
-    }
-    return n;
-  };
-  // wait until at most n of this wave's loads are outstanding
-  auto wait_vm = [&](int n) {
-    if (n >= 2 * kI)
-      pp_wait_vm<2 * kI>();
-    else if (n >= kI)
-      pp_wait_vm<kI>();
-    else
-      pp_wait_vm<0>();
-  };
-  using Y = std::integral_constant<bool, true>;
-  using N = std::integral_constant<bool, false>;
-
-  if (T > 0) {
-    if (grp == 0) {
-      ld.template issue<false>(a, w, t_begin * kBN, kslot(0));
-      if (T > 1) ld.template issue<false>(a, w, (t_begin + 1) * kBN, kslot(1));
-      ld.template issue<true>(a, w, t_begin * kBN, vslot(0));
-      wait_vm(T > 1 ? 2 * kI : kI);  // K(0) has landed
-    }
-    pp_barrier();
-    if (grp != 0) pp_barrier();  // group 1 runs one phase behind
-    int n = 0;
-#if FA2_PP_DMA_IN_M
-    if (grp == 0) n = issue_iter(0);
-#endif
-    phase_m(N{}, Y{}, 0);
-    pp_barrier();
-    for (int i = 0; i + 1 < T; ++i) {
-#if !FA2_PP_DMA_IN_M
-      if (grp == 0) n = issue_iter(i);
-#endif
-      phase_v(i);
-      // K(i+1) and V(i) (read from M(i+1) on) have landed; the loads of
-      // the current issue may still be in flight
-      if (grp == 0) wait_vm(n);
-      pp_barrier();
-#if FA2_PP_DMA_IN_M
-      if (grp == 0) n = issue_iter(i + 1);
-#endif
-      phase_m(Y{}, Y{}, i + 1);
-      pp_barrier();
-    }
-    phase_v(T - 1);
-    if (grp == 0) pp_wait_vm<0>();  // V(T-1), read by the last PV
-    pp_barrier();
-    phase_m(Y{}, N{}, T);
-    if (grp == 0) pp_barrier();  // pairs with group 1's last barrier
-    // every wave is past its last LDS read: the whole LDS is free
-    if (S == 1) pp_barrier();
-  }
-
-  if (!hok) return;
-  const float l_tot = sum_xor32(l_run);
-  if (S == 1) {
-    static_assert(kPPWaves * OStage<D>::kBytes <= sizeof(lds), "O staging exceeds LDS");
-    const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
-    store_o_staged<DT, D>(o, inv, lds + wave * OStage<D>::kBytes, a.o, o_base, a.o_ss, wq_first,
-                          w.Lq, lane);
-  } else {
-    // partials go to the slot the one-head-per-unit layout gives this head
-    // (decode_work with heads = 1), which the combine kernel reads
-    const int unit = ((w.pair / kXcds) * group + w.hg + grp) * kXcds + w.pair % kXcds;
-    const int64_t slot = static_cast<int64_t>(split) * a.part_slots + unit;
-    const int r = wq * kWaveRows + l32;
-    if (hi == 0) {
-      float* ml = a.part_ml + (slot * kBM + r) * 2;
-      ml[0] = m_run;
-      ml[1] = l_tot;
-    }
-    float* po = a.part_o + (slot * kBM + r) * D + hi * 4;
-#pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
-            (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
+    if (!has_next) break;
+    gb += T;
+    pre = pre_next;
+    cur = nxt;
+    r = rn;
   }
 }
 
