@@ -45,7 +45,12 @@ METRIC = "TFLOP/s + % of bf16 MFMA peak, flash_attention_v2 causal GQA seq2048 d
 DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16, "f16": torch.float16,
           "fp32": torch.float32, "f32": torch.float32}
 DTYPE_NAME = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
+METRIC_HBM = "GB/s of HBM (algorithmic bytes), {kind} {config}"
 DESCR = {
+    "d1": "d1 paged decode B16 QH8 KVH8 N8192 D64 page16",
+    "d2": "d2 paged decode 64 seqs ctx~U[512,8192] page16 Hq32 Hkv8 D128",
+    "s1": "s1 paged speculative decode causal M8 B16 QH8 KVH8 N8192+8 D64 page16",
+    "s2": "s2 paged speculative decode causal M8 64 seqs ctx~U[512,8192]+8 page16 Hq32 Hkv8 D128",
     "c1": "c1 dense causal MHA B1 H8 L512 D64",
     "c2": "c2 dense causal GQA B2 Hq32 Hkv8 L2048 D128",
     "c3": "c3 ragged causal self 16 seqs L~U[128,4096] Hq32 Hkv8 D128",
@@ -79,6 +84,11 @@ def cpu_baseline(w: W.Workload, budget_s: float = 20.0):
         return 4.0 * w.head_dim * g * W.visible_pairs(w.q_lens[b], w.kv_lens[b], w.is_causal,
                                                        w.causal_alignment)
 
+    es = torch.tensor([], dtype=w.dtype).element_size()
+
+    def unit_bytes(b):  # q, o of the group's heads; k, v of one kv head
+        return es * w.head_dim * (2 * w.q_lens[b] * g + 2 * w.kv_lens[b])
+
     # time one unit to size the sample
     t0 = time.perf_counter()
     unit_call(*units[0])
@@ -87,6 +97,7 @@ def cpu_baseline(w: W.Workload, budget_s: float = 20.0):
     step = max(1, len(units) // n)
     sample = units[::step][:n]
     fl = sum(unit_flops(b) for b, _ in sample)
+    nb = sum(unit_bytes(b) for b, _ in sample)
     for b, kh in sample[:1]:
         unit_call(b, kh)  # warmup
     times = []
@@ -96,14 +107,18 @@ def cpu_baseline(w: W.Workload, budget_s: float = 20.0):
             unit_call(b, kh)
         times.append(time.perf_counter() - t0)
     med = sorted(times)[1]
+    if w.kind != "prefill":
+        value, unit, amount = nb / med / 1e9, "GB/s", f"{nb / 1e6:.1f} MB"
+    else:
+        value, unit, amount = fl / med / 1e12, "TFLOP/s", f"{fl / 1e9:.1f} GFLOP"
     return {
-        "value": round(fl / med / 1e12, 4),
-        "unit": "TFLOP/s",
+        "value": round(value, 4),
+        "unit": unit,
         "cores": cores,
         "kind": "port",
         "sample": f"{len(sample)} of {len(units)} (sequence, kv-head group) units of "
                   f"{w.name}, fp32 SDPA per sequence with repeat_interleaved KV heads, "
-                  f"{fl / 1e9:.1f} GFLOP per rep, median of 3",
+                  f"{amount} per rep, median of 3",
     }
 
 
@@ -159,7 +174,7 @@ def main(argv=None):
               file=sys.stderr)
         return 2
 
-    from kernels import _fa2
+    from kernels import _fa2, decode_attention, speculative_decode_attention
     from kernels.attention import flash_attention_v2
 
     _fa2.lib()
@@ -173,8 +188,11 @@ def main(argv=None):
     nbytes = W.hbm_bytes(w)
     flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if args.flush else None
 
+    fn = {"prefill": flash_attention_v2, "decode": decode_attention,
+          "speculative": speculative_decode_attention}[w.kind]
+
     def step():
-        return flash_attention_v2(w.q, w.k, w.v, **kw)
+        return fn(w.q, w.k, w.v, **kw)
 
     print(f"bench: {DESCR[args.config]} {DTYPE_NAME[w.dtype]} warmup={args.warmup} "
           f"steps={args.steps}", file=sys.stderr, flush=True)
@@ -209,15 +227,20 @@ def main(argv=None):
         torch.cuda.synchronize()
         kern_avg = sum(a.elapsed_time(b) for a, b in ev) / args.steps
         ms_per_step = kern_avg  # wall clock would include the flush writes
-    value = fl / (ms_per_step * 1e-3) / 1e12
-    achieved = fl / (kern_avg * 1e-3) / 1e12
     bound = "mfma" if fl / nbytes > (PEAK_TFLOPS * 1e12) / (PEAK_HBM_GBS * 1e9) else "hbm"
+    if bound == "mfma":
+        metric, unit, peak, work = METRIC, "TFLOP/s", PEAK_TFLOPS, fl / 1e12
+    else:
+        metric = METRIC_HBM.format(kind=fn.__name__, config=args.config)
+        unit, peak, work = "GB/s", PEAK_HBM_GBS, nbytes / 1e9
+    value = work / (ms_per_step * 1e-3)
+    achieved = work / (kern_avg * 1e-3)
 
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 2),
-        "unit": "TFLOP/s",
-        "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "unit": unit,
+        "pct_of_peak": round(100.0 * value / peak, 2),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -240,12 +263,13 @@ def main(argv=None):
         "roofline": {
             "bound": bound,
             "achieved": round(achieved, 2),
-            "peak": round(PEAK_TFLOPS, 1),
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "peak": round(peak, 1),
+            "unit": unit,
+            "frac": round(achieved / peak, 4),
             "traffic": hbm_traffic(args.config, DTYPE_NAME[w.dtype]),
             "kernel_ms_avg": round(kern_avg, 5),
             "hbm_gbs_algorithmic": round(nbytes / (kern_avg * 1e-3) / 1e9, 1),
+            "tflops_algorithmic": round(fl / (kern_avg * 1e-3) / 1e12, 2),
         },
         "cpu_baseline": None,
     }

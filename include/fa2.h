@@ -75,7 +75,11 @@ enum fa2_status {
   FA2_ERR_WORKSPACE = 10,      /* workspace missing or smaller than required   */
   FA2_ERR_SPLITS = 11,         /* num_splits out of range                       */
   FA2_ERR_HIP = 12,            /* a HIP runtime call or a launch failed         */
-  FA2_ERR_TOO_LARGE = 13       /* a size exceeds the kernels' 32-bit counters  */
+  FA2_ERR_TOO_LARGE = 13,      /* a size exceeds the kernels' 32-bit counters  */
+  FA2_ERR_Q_LAYOUT = 14        /* decode: the rows of the query heads sharing a
+                                  kv head are not one strided run
+                                  (q_sh != q_len * q_ss, likewise o; with M = 1
+                                  pass q_ss = q_sh)                             */
 };
 
 /* Supported head dims (the reference accepts any power of two via
@@ -138,6 +142,43 @@ int fa2_fwd(const fa2_params* p, void* stream);
 
 /* Static, human-readable text for a status code. */
 const char* fa2_strerror(int status);
+
+/* ---- decode and speculative decode ---------------------------------------
+ *
+ * The same parameter block serves `decode_attention` and
+ * `speculative_decode_attention`, with these meanings:
+ *   q, o      [B, Hq, M, D] for EVERY layout (M = q_len >= 1 query tokens per
+ *             sequence: 1 for decode, the draft length for speculative decode;
+ *             `decode_attention`'s [B, Hq, D] is M = 1);
+ *   k, v      per `layout` exactly as above (dense [B,Hkv,N,D]; ragged
+ *             [Tkv,Hkv,D] with kv_indptr = prefix sums [B+1]; paged caches
+ *             with kv_indptr = lengths [B] and block tables); q_indptr unused;
+ *   mask      FA2_MASK_NONE, or FA2_MASK_CAUSAL_BOTTOM_RIGHT for the
+ *             speculative causal mask: query token m of a sequence of Lk keys
+ *             sees key j iff j <= Lk - M + m (the last M keys are the drafts);
+ *             FA2_MASK_CAUSAL_TOP_LEFT is rejected;
+ *   layout of q/o: the Hq/Hkv heads of one kv head must be one run of rows,
+ *             q_sh == q_len * q_ss (true for contiguous tensors; for M = 1 the
+ *             row stride is the head stride, q_ss = q_sh); likewise o.
+ * Internally the Hq/Hkv query heads that share a kv head are computed as the
+ * rows of one unit, so each K/V row is read from HBM once per kv head.  The
+ * computation is that of fa2_fwd (same dtypes and rounding, fp32 softmax
+ * statistics).  A sequence with no visible key gives NaN rows (the
+ * reference's 0/0, kernels/decode.py:318-327).
+ *
+ * Reference interfaces replaced:
+ *   kernels/decode.py:203-331             `decode_attention` host wrapper
+ *   kernels/decode.py:22-170, 173-200     split kernel + merge kernel
+ *   kernels/speculative_decode.py:228-365 `speculative_decode_attention`
+ *   kernels/speculative_decode.py:22-225  split kernel + merge kernel      */
+
+/* Bytes of device workspace fa2_decode_fwd needs for `p`. */
+int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes);
+
+/* Validate `p` and enqueue decode / speculative-decode attention on `stream`
+ * (a hipStream_t).  Returns FA2_OK or an error code; validation errors are
+ * reported before any launch.  No allocation, no host synchronisation. */
+int fa2_decode_fwd(const fa2_params* p, void* stream);
 
 /* Version of this ABI (bumped on any change to fa2_params).  No counterpart
  * in the reference: lets a binding refuse a library it was not written for. */

@@ -1,4 +1,5 @@
-"""CPU oracle for ``flash_attention_v2`` (harsh-vsingh/triton-kernels).
+"""CPU oracle for ``flash_attention_v2``, ``decode_attention`` and
+``speculative_decode_attention`` (harsh-vsingh/triton-kernels).
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
 the ``cpu_baseline`` leg of ``bench.py`` import this package, and only as the
@@ -19,7 +20,14 @@ Two restatements live here:
   (``tests/test_attention.py:80-98``), and the explicit bottom-right mask
   construction of ``tests/test_speculative_decode.py:101-114``.
 * :func:`attn_tolerances` - the tolerance formula of
-  ``tests/test_attention.py:20-30``.
+  ``tests/test_attention.py:20-30`` (identical in ``tests/test_decode.py:20-30``
+  and ``tests/test_speculative_decode.py:20-30``).
+* :func:`oracle_decode` - the C restatement of ``decode_attention`` and
+  ``speculative_decode_attention`` (``kernels/decode.py``,
+  ``kernels/speculative_decode.py``: split kernel with strided key blocks,
+  guarded max of the speculative kernel, log-sum-exp merge), and
+  :func:`sdpa_decode_reference` / :func:`sdpa_speculative_reference`, those
+  suites' own SDPA oracles.
 
 How the C restatement is pinned (tests/test_oracle.py): against fp64 SDPA
 (a library routine) on every layout/mask/topology, against committed golden
@@ -95,6 +103,8 @@ def _load():
             lib = ctypes.CDLL(_LIB_PATH)
             lib.fa2o_fwd.argtypes = [ctypes.POINTER(_Args)]
             lib.fa2o_fwd.restype = ctypes.c_int
+            lib.fa2o_decode.argtypes = [ctypes.POINTER(_Args), ctypes.c_int]
+            lib.fa2o_decode.restype = ctypes.c_int
             lib.fa2o_round_f16.argtypes = [ctypes.c_float]
             lib.fa2o_round_f16.restype = ctypes.c_float
             lib.fa2o_round_bf16.argtypes = [ctypes.c_float]
@@ -175,8 +185,73 @@ def oracle_attention(q, k, v, *, is_causal=False, q_indptr=None, kv_indptr=None,
     return out
 
 
+def oracle_decode(q, k, v, *, causal=False, kv_indptr=None, k_block_table=None,
+                  v_block_table=None, kv_page_size=None, spec=None, operand_round="none",
+                  p_round="none", block_n=64, split_k=1, scale=None, mutation=0):
+    """C restatement of ``decode_attention`` (q ``[B,QH,D]``) or
+    ``speculative_decode_attention`` (q ``[B,QH,M,D]``) on CPU; fp32 output
+    of q's shape.
+
+    Same arguments and layout rules as the reference entry points
+    (kernels/decode.py:203-331, kernels/speculative_decode.py:228-365).
+    ``spec`` selects the speculative kernel's guarded max (default: True for
+    4-D q).  Default rounding "none" is the reference's fp32 arithmetic;
+    ``block_n`` / ``split_k`` are its autotuned block and split factor.
+    """
+    if spec is None:
+        spec = q.dim() == 4
+    q4 = q if q.dim() == 4 else q.unsqueeze(2)
+    paged = k_block_table is not None
+    ragged = (kv_indptr is not None) and not paged
+    qf = q4.detach().to("cpu", torch.float32).contiguous()
+    kf = k.detach().to("cpu", torch.float32)
+    vf = v.detach().to("cpu", torch.float32)
+    if paged and kf.dim() == 4:  # [pages, page, KVH, D]
+        kf = kf.reshape(-1, kf.shape[2], kf.shape[3])
+        vf = vf.reshape(-1, vf.shape[2], vf.shape[3])
+    kf = kf.contiguous()
+    vf = vf.contiguous()
+    out = torch.zeros_like(qf)
+    a = _Args()
+    a.layout = LAYOUT["paged" if paged else ("ragged" if ragged else "dense")]
+    a.mask = MASK["bottom_right"] if causal else 0
+    a.operand_round = ROUND[operand_round]
+    a.p_round = ROUND[p_round]
+    a.block_m, a.block_n, a.split_k = 1, block_n, split_k
+    a.mutation = int(mutation)
+    a.batch, a.q_heads, a.q_len, a.head_dim = qf.shape
+    keep = []
+    if paged:
+        a.kv_heads, a.kv_len = kf.shape[1], 0
+        kvi = kv_indptr.detach().to("cpu", torch.int32).contiguous()
+        kt = k_block_table.detach().to("cpu", torch.int32).contiguous()
+        vt = v_block_table.detach().to("cpu", torch.int32).contiguous()
+        keep += [kvi, kt, vt]
+        a.kv_indptr, a.k_table, a.v_table = kvi.data_ptr(), kt.data_ptr(), vt.data_ptr()
+        a.k_table_stride, a.v_table_stride = kt.stride(0), vt.stride(0)
+        a.page_size = int(kv_page_size)
+    elif ragged:
+        a.kv_heads, a.kv_len = kf.shape[1], kf.shape[0]
+        kvi = kv_indptr.detach().to("cpu", torch.int32).contiguous()
+        keep.append(kvi)
+        a.kv_indptr = kvi.data_ptr()
+    else:
+        a.kv_heads, a.kv_len = kf.shape[1], kf.shape[2]
+    a.q_sb, a.q_sh, a.q_ss = _strides3(qf)
+    a.k_sb, a.k_sh, a.k_ss = _strides3(kf)
+    a.v_sb, a.v_sh, a.v_ss = _strides3(vf)
+    a.o_sb, a.o_sh, a.o_ss = _strides3(out)
+    a.q, a.k, a.v, a.o = qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), out.data_ptr()
+    a.scale = float(a.head_dim ** -0.5 if scale is None else scale)
+    rc = _load().fa2o_decode(ctypes.byref(a), int(bool(spec)))
+    if rc != 0:
+        raise RuntimeError(f"fa2o_decode failed with code {rc}")
+    return out if q.dim() == 4 else out.squeeze(2)
+
+
 # ---------------------------------------------------------------------------
-# The reference test suite's oracle (tests/test_attention.py:80-98).
+# The reference test suites' oracles (tests/test_attention.py:80-98,
+# tests/test_decode.py:75-99, tests/test_speculative_decode.py:69-126).
 # ---------------------------------------------------------------------------
 
 def sdpa_reference(qs, ks, vs, QH, KVH, is_causal, dtype=torch.float32):
@@ -224,6 +299,51 @@ def sdpa_reference_bottom_right(qs, ks, vs, QH, KVH, dtype=torch.float32):
         empty = ~mask.any(dim=1)
         out[empty] = float("nan")
         refs.append(out)
+    return refs
+
+
+def sdpa_decode_reference(qs, ks, vs, QH, KVH, dtype=torch.float32):
+    """tests/test_decode.py:75-99: per sequence, q ``[QH,D]`` against k/v
+    ``[L,KVH,D]``, upcast, KV heads repeat_interleaved; returns ``[QH,D]``."""
+    refs = []
+    for q, k, v in zip(qs, ks, vs):
+        q_ref = q.unsqueeze(0).unsqueeze(2).to(dtype)
+        k_ref = k.transpose(0, 1).unsqueeze(0).to(dtype)
+        v_ref = v.transpose(0, 1).unsqueeze(0).to(dtype)
+        if QH != KVH:
+            g = QH // KVH
+            k_ref = k_ref.repeat_interleave(g, dim=1)
+            v_ref = v_ref.repeat_interleave(g, dim=1)
+        refs.append(F.scaled_dot_product_attention(q_ref, k_ref, v_ref).squeeze(0).squeeze(1))
+    return refs
+
+
+def sdpa_speculative_reference(qs, ks, vs, dks, dvs, QH, KVH, causal, dtype=torch.float32):
+    """tests/test_speculative_decode.py:69-126: per sequence, q ``[QH,M,D]``
+    against the context k/v ``[L,KVH,D]`` plus, when causal, the M draft
+    rows ``dks``/``dvs`` ``[M,KVH,D]`` appended and hidden from earlier drafts
+    (mask row i: keys ``> L + i`` off); returns ``[QH,M,D]``."""
+    refs = []
+    for q, k, v, dk, dv in zip(qs, ks, vs, dks, dvs):
+        q_ref = q.unsqueeze(0).to(dtype)
+        k_ref = k.transpose(0, 1).unsqueeze(0).to(dtype)
+        v_ref = v.transpose(0, 1).unsqueeze(0).to(dtype)
+        if causal:
+            k_ref = torch.cat([k_ref, dk.transpose(0, 1).unsqueeze(0).to(dtype)], dim=2)
+            v_ref = torch.cat([v_ref, dv.transpose(0, 1).unsqueeze(0).to(dtype)], dim=2)
+        if QH != KVH:
+            g = QH // KVH
+            k_ref = k_ref.repeat_interleave(g, dim=1)
+            v_ref = v_ref.repeat_interleave(g, dim=1)
+        mask = None
+        if causal:
+            M = q_ref.shape[2]
+            N = k_ref.shape[2] - M
+            mask = torch.ones((M, N + M), dtype=torch.bool)
+            for i in range(M):
+                mask[i, N + i + 1:] = False
+        refs.append(F.scaled_dot_product_attention(q_ref, k_ref, v_ref, attn_mask=mask,
+                                                   is_causal=False).squeeze(0))
     return refs
 
 

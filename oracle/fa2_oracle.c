@@ -239,3 +239,145 @@ int fa2o_fwd(const fa2o_args* a) {
   free(qv); free(sc); free(acc); free(mm); free(ll);
   return 0;
 }
+
+/* ---- decode_attention / speculative_decode_attention --------------------
+ *
+ * Restates kernels/decode.py (spec = 0) and kernels/speculative_decode.py
+ * (spec = 1).  q and o are [B, Hq, M, D] for every K/V layout (decode: M = 1,
+ * the reference's [B, Hq, D]); K/V follow a->layout as above, with
+ * kv_indptr = prefix sums (ragged, decode.py:57-66) or lengths (paged,
+ * decode.py:68-75); the dense layout gives every sequence kv_len keys
+ * (decode.py:55).  Per (sequence, q head, query m):
+ *   - key blocks of BLOCK_N, block i handled by split i % S (the loop
+ *     `while pid0 < total: ... pid0 += SPLIT_K`, decode.py:88-162,
+ *     speculative_decode.py:95-178);
+ *   - scores in fp32, scaled, -inf past the sequence end (decode.py:146-149)
+ *     and, speculative + causal, for drafts after m: key n is hidden iff
+ *     n >= Lk - M and n - (Lk - M) > m (speculative_decode.py:89, 155-160);
+ *   - decode: m' = max(m, max_j s_j), alpha = exp(m - m'), P = exp(s - m'),
+ *     acc = acc*alpha + sum P v, l = l*alpha + sum P (decode.py:151-160);
+ *   - speculative: the same with a guarded max - while no key has been
+ *     visible the stabiliser is 0 and alpha, P are 0
+ *     (speculative_decode.py:165-177);
+ *   - merge: g = max_s m_s, O = sum_s e^(m_s - g) acc_s / sum_s e^(m_s - g) l_s
+ *     (decode.py:188-200, speculative_decode.py:211-226); a sequence with no
+ *     visible key gives 0/0 = NaN.
+ * The reference computes these in fp32 from upcast inputs (decode.py:96-144);
+ * its speculative kernel forms Q K^T and P V with tl.dot on fp32 operands,
+ * which NVIDIA hardware may run in TF32: the restatement keeps those
+ * products in fp32 (operand_round / p_round "none"), a difference far below
+ * the reference tolerance.  operand_round / p_round select the rounding of
+ * this build's MFMA kernels for the strict error-floor comparison. */
+int fa2o_decode(const fa2o_args* a, int spec) {
+  if (!a || !a->q || !a->k || !a->v || !a->o) return 1;
+  if (a->q_heads <= 0 || a->kv_heads <= 0 || a->q_heads % a->kv_heads) return 2;
+  if (a->block_n <= 0 || a->split_k <= 0 || a->q_len <= 0) return 3;
+  const int64_t D = a->head_dim, BN = a->block_n, S = a->split_k, M = a->q_len;
+  const int opr = a->operand_round, prd = a->p_round;
+  const int causal = a->mask != FA2O_MASK_NONE;
+
+  float* qv = (float*)malloc(sizeof(float) * D);
+  float* sc = (float*)malloc(sizeof(float) * BN);
+  float* acc = (float*)malloc(sizeof(float) * S * D);
+  float* mm = (float*)malloc(sizeof(float) * S);
+  float* ll = (float*)malloc(sizeof(float) * S);
+  if (!qv || !sc || !acc || !mm || !ll) {
+    free(qv); free(sc); free(acc); free(mm); free(ll);
+    return 4;
+  }
+  for (int64_t b = 0; b < a->batch; ++b) {
+    for (int64_t h = 0; h < a->q_heads; ++h) {
+      const int64_t kvh = (a->mutation == FA2O_MUT_HEAD_MAP) ? h % a->kv_heads
+                                                              : h * a->kv_heads / a->q_heads;
+      seq_t s;
+      s.Lq = M;
+      s.q_base = b * a->q_sb + h * a->q_sh;
+      s.o_base = b * a->o_sb + h * a->o_sh;
+      if (a->layout == FA2O_LAYOUT_DENSE) {
+        s.Lk = a->kv_len;
+        s.k_base = b * a->k_sb + kvh * a->k_sh;
+        s.v_base = b * a->v_sb + kvh * a->v_sh;
+      } else if (a->layout == FA2O_LAYOUT_RAGGED) {
+        const int64_t ks = a->kv_indptr[b];
+        s.Lk = a->kv_indptr[b + 1] - ks;
+        s.k_base = ks * a->k_ss + kvh * a->k_sh;
+        s.v_base = ks * a->v_ss + kvh * a->v_sh;
+      } else {
+        s.Lk = a->kv_indptr[b];
+        s.k_base = kvh * a->k_sh;
+        s.v_base = kvh * a->v_sh;
+      }
+      if (s.Lk < 0) s.Lk = 0;
+      const int64_t draft_start = s.Lk - M;
+      const int64_t total = (s.Lk + BN - 1) / BN;
+      for (int64_t i = 0; i < M; ++i) {
+        for (int64_t d = 0; d < D; ++d) qv[d] = rnd(a->q[s.q_base + i * a->q_ss + d], opr);
+        for (int64_t sp = 0; sp < S; ++sp) {
+          float m = -INFINITY, l = 0.f;
+          float* ac = acc + sp * D;
+          for (int64_t d = 0; d < D; ++d) ac[d] = 0.f;
+          for (int64_t kb = sp; kb < total; kb += S) {
+            float bmax = -INFINITY;
+            for (int64_t j = 0; j < BN; ++j) {
+              const int64_t n = kb * BN + j;
+              int ok = n < s.Lk;
+              if (ok && causal && n >= draft_start)
+                ok = (a->mutation == FA2O_MUT_CAUSAL_OFF1) ? n - draft_start < i
+                                                           : n - draft_start <= i;
+              if (!ok) {
+                sc[j] = -INFINITY;
+                continue;
+              }
+              const float* kr = a->k + key_row(a, &s, b, n, 0);
+              float dot = 0.f;
+              for (int64_t d = 0; d < D; ++d) dot += qv[d] * rnd(kr[d], opr);
+              sc[j] = (a->mutation == FA2O_MUT_NO_SCALE) ? dot : dot * a->scale;
+              if (sc[j] > bmax) bmax = sc[j];
+            }
+            float mnew = m > bmax ? m : bmax;
+            float alpha;
+            int none = 0;
+            if (spec) {
+              none = mnew == -INFINITY;
+              if (none) mnew = 0.f;
+              alpha = none ? 0.f : expf(m - mnew);
+            } else {
+              alpha = expf(m - mnew);
+            }
+            float psum = 0.f;
+            if (a->mutation != FA2O_MUT_NO_RESCALE)
+              for (int64_t d = 0; d < D; ++d) ac[d] *= alpha;
+            for (int64_t j = 0; j < BN; ++j) {
+              const int64_t n = kb * BN + j;
+              const float p = none ? 0.f : rnd(expf(sc[j] - mnew), prd);
+              psum += p;
+              if (n < s.Lk && p != 0.f) {
+                const float* vr = (a->mutation == FA2O_MUT_K_AS_V) ? a->k + key_row(a, &s, b, n, 0)
+                                                                   : a->v + key_row(a, &s, b, n, 1);
+                for (int64_t d = 0; d < D; ++d) ac[d] += p * rnd(vr[d], opr);
+              }
+            }
+            l = l * alpha + psum;
+            m = mnew;
+          }
+          mm[sp] = m;
+          ll[sp] = l;
+        }
+        float g = -INFINITY;
+        for (int64_t sp = 0; sp < S; ++sp) g = mm[sp] > g ? mm[sp] : g;
+        float tot = 0.f;
+        float* orow = a->o + s.o_base + i * a->o_ss;
+        for (int64_t d = 0; d < D; ++d) orow[d] = 0.f;
+        for (int64_t sp = 0; sp < S; ++sp) {
+          const float w = expf(mm[sp] - g);
+          tot += ll[sp] * w;
+          for (int64_t d = 0; d < D; ++d) orow[d] += acc[sp * D + d] * w;
+        }
+        for (int64_t d = 0; d < D; ++d) orow[d] = orow[d] / tot;
+      }
+    }
+  }
+  free(qv); free(sc); free(acc); free(mm); free(ll);
+  return 0;
+}
+

@@ -1,6 +1,8 @@
 /*
  * fa2_oracle.h - CPU restatement of the reference flash_attention_v2
- * (harsh-vsingh/triton-kernels kernels/attention.py:430-927).
+ * (harsh-vsingh/triton-kernels kernels/attention.py:430-927), decode_attention
+ * (kernels/decode.py:22-331) and speculative_decode_attention
+ * (kernels/speculative_decode.py:22-365).
  *
  * TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and the
  * CPU-baseline leg of bench.py as the checker; never by the product path.
@@ -57,6 +59,11 @@ typedef struct fa2o_args {
 } fa2o_args;
 
 int fa2o_fwd(const fa2o_args* a);
+/* decode_attention (spec = 0, kernels/decode.py) and
+ * speculative_decode_attention (spec = 1, kernels/speculative_decode.py):
+ * q/o [B, Hq, M = q_len, D] for every K/V layout; mask NONE or, speculative
+ * causal, BOTTOM_RIGHT (draft m sees key n iff n <= Lk - M + m). */
+int fa2o_decode(const fa2o_args* a, int spec);
 float fa2o_round_f16(float x);
 float fa2o_round_bf16(float x);
 

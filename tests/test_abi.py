@@ -31,16 +31,16 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layout_matches():
     assert _fa2.lib().fa2_params_size() == ctypes.sizeof(_fa2.Fa2Params)
-    assert _fa2.lib().fa2_abi_version() == 1
+    assert _fa2.lib().fa2_abi_version() == _fa2.ABI_VERSION == 2
 
 
 def test_strerror_for_every_code():
     seen = set()
-    for code in range(14):
+    for code in range(15):
         msg = _fa2.lib().fa2_strerror(code).decode()
         assert msg and "unknown" not in msg
         seen.add(msg)
-    assert len(seen) == 14
+    assert len(seen) == 15
     assert "unknown" in _fa2.lib().fa2_strerror(999).decode()
 
 
@@ -137,3 +137,57 @@ def test_product_path_does_not_import_the_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "from oracle" not in text, f
                 assert "fa2_oracle" not in text, f
+
+
+# ---- decode / speculative decode entry points ------------------------------
+
+def decode_params(M=1, **kw):
+    """q/o [B=2, Hq=8, M, D=128] over a dense K/V [2, 2, 300, 128]."""
+    p = dense_params(mask=0, num_splits=0, q_len=M)
+    p.q_sb, p.q_sh, p.q_ss = 8 * M * 128, M * 128, 128 if M > 1 else M * 128
+    p.o_sb, p.o_sh, p.o_ss = p.q_sb, p.q_sh, p.q_ss
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def rc_dec(p):
+    n = ctypes.c_size_t(0)
+    r1 = _fa2.lib().fa2_decode_workspace_size(ctypes.byref(p), ctypes.byref(n))
+    r2 = _fa2.lib().fa2_decode_fwd(ctypes.byref(p), None)
+    return r1, r2, n.value
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_decode_workspace_ok(M):
+    r1, _, n = rc_dec(decode_params(M, q=0))
+    assert r1 == 0
+    # 8 query heads share 2 kv heads: units = B * Hkv = 4, so the KV sweep is split
+    assert n > 0
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("mask", 1, 4),     # top-left causal has no decode meaning
+    ("mask", 3, 4),
+    ("q_sh", 256, 14),  # heads of a group are not one run of rows
+    ("o_ss", 64, 14),
+    ("head_dim", 96, 6),
+    ("num_splits", 65, 11),
+])
+def test_decode_validation_errors(field, value, code):
+    r1, r2, _ = rc_dec(decode_params(4, **{field: value}))
+    assert r1 == code and r2 == code
+
+
+def test_decode_ragged_needs_only_kv_indptr():
+    p = decode_params(1, layout=1)
+    assert rc_dec(p)[0] == 9           # kv_indptr missing
+    p.kv_indptr = 0x1000               # never dereferenced on the host
+    assert rc_dec(p)[0] == 0           # q_indptr is not needed
+
+
+def test_decode_mqa_m1_any_head_stride():
+    """One query head per kv head: the group is one row, any head stride."""
+    p = decode_params(1, kv_heads=8, q_sh=256, q_ss=128, o_sh=256, o_ss=128,
+                      k_sb=8 * 300 * 128, v_sb=8 * 300 * 128)
+    assert rc_dec(p)[0] == 0

@@ -100,6 +100,13 @@ struct KArgs {
   const int32_t* work_count;
   float* part_ml;       // split partials: (m, l) per row
   float* part_o;        // split partials: unnormalised O per row
+  int32_t part_rows;    // split partials: rows per slot (kBM; the row count in packed mode)
+  // Packed-head (decode) mode when > 0: q/o are [B, Hq, pack_m, D] for every
+  // K/V layout, and the Hq/Hkv query heads of one kv head form the rows of a
+  // single unit, row r = (head in group) * pack_m + draft position; q_len is
+  // then the unit's row count Hq/Hkv * pack_m.  Causal is bottom-right per
+  // draft position: row r sees key j iff j <= Lk - pack_m + r % pack_m.
+  int32_t pack_m;
 };
 
 // ---------------------------------------------------------------------------
@@ -256,7 +263,7 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1
   Work w;
   w.valid = true;
   const int group = a.hq / a.hkv;
-  const int units = (group + heads - 1) / heads;
+  const int units = a.pack_m > 0 ? 1 : (group + heads - 1) / heads;
   const int p = L % kXcds;
   const int rest = L / kXcds;
   const int g = rest % units;
@@ -274,7 +281,7 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1
     const int rank = item / a.batch;
     w.b = item % a.batch;
     // heaviest q-blocks first under a causal mask
-    w.qblk = (a.mask != FA2_MASK_NONE) ? (a.nqb - 1 - rank) : rank;
+    w.qblk = (a.mask != FA2_MASK_NONE && a.pack_m == 0) ? (a.nqb - 1 - rank) : rank;
     w.Lq = a.q_len;
     w.Lk = a.kv_len;
     w.q_base = w.b * a.q_sb + w.h * a.q_sh;
@@ -290,12 +297,18 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1
     w.b = it.x;
     w.qblk = it.y;
     if constexpr (MODE == FA2_LAYOUT_RAGGED) {
-      const int qs = a.q_indptr[w.b];
       const int ks = a.kv_indptr[w.b];
-      w.Lq = a.q_indptr[w.b + 1] - qs;
       w.Lk = a.kv_indptr[w.b + 1] - ks;
-      w.q_base = qs * a.q_ss + w.h * a.q_sh;
-      w.o_base = qs * a.o_ss + w.h * a.o_sh;
+      if (a.pack_m > 0) {  // decode: dense q/o over a ragged K/V
+        w.Lq = a.q_len;
+        w.q_base = w.b * a.q_sb + w.h * a.q_sh;
+        w.o_base = w.b * a.o_sb + w.h * a.o_sh;
+      } else {
+        const int qs = a.q_indptr[w.b];
+        w.Lq = a.q_indptr[w.b + 1] - qs;
+        w.q_base = qs * a.q_ss + w.h * a.q_sh;
+        w.o_base = qs * a.o_ss + w.h * a.o_sh;
+      }
       w.k_base = ks * a.k_ss + w.kvh * a.k_sh;
       w.v_base = ks * a.v_ss + w.kvh * a.v_sh;
     } else {  // paged: dense q/o, lengths in kv_indptr
@@ -309,8 +322,15 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1
   }
   if (w.Lk < 0) w.Lk = 0;
   if (w.Lq < 0) w.Lq = 0;
-  w.off = (a.mask == FA2_MASK_CAUSAL_BOTTOM_RIGHT) ? (w.Lk - w.Lq) : 0;
+  w.off = (a.mask == FA2_MASK_CAUSAL_BOTTOM_RIGHT) ? (w.Lk - (a.pack_m > 0 ? a.pack_m : w.Lq))
+                                                   : 0;
   return w;
+}
+
+// Query position of unit row `row` on the causal diagonal: the row itself,
+// or its draft position in packed-head mode.
+__device__ __forceinline__ int diag_row(const KArgs& a, int row) {
+  return a.pack_m > 0 ? row % a.pack_m : row;
 }
 
 // Number of keys a q-block [q0, q0+BM) can see (exclusive end), >= 0.
@@ -319,6 +339,12 @@ __device__ __forceinline__ int kv_end_for_block(int mask, int q0, int Lq, int Lk
   int qe = min(q0 + kBM, Lq);
   int e = min(Lk, qe + off);
   return e > 0 ? e : 0;
+}
+
+// The same for a unit; in packed-head mode the last draft position of every
+// block sees the whole sequence.
+__device__ __forceinline__ int kv_end_for_unit(const KArgs& a, int q0, int Lq, int Lk, int off) {
+  return a.pack_m > 0 ? Lk : kv_end_for_block(a.mask, q0, Lq, Lk, off);
 }
 
 // ---------------------------------------------------------------------------
@@ -520,7 +546,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
   const int S = a.num_splits;
 
   // KV tile range of this split.
-  const int kv_end = kv_end_for_block(a.mask, q0, w.Lq, w.Lk, w.off);
+  const int kv_end = kv_end_for_unit(a, q0, w.Lq, w.Lk, w.off);
   const int ntiles = (kv_end + kBN - 1) / kBN;
   const int t_begin = (ntiles * split) / S;
   const int t_end = (ntiles * (split + 1)) / S;
@@ -551,7 +577,10 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
 
   uint16_t* ks_base = lds;
   uint16_t* vt_base = lds + 2 * L::kKTile;
+  // first row of the wave; its rows' smallest diagonal position and this lane's
   const int wq_first = q0 + wave * kWaveRows;
+  const int wq_diag = a.pack_m > 0 ? 0 : wq_first;
+  const int qdiag = diag_row(a, qrow);
   const bool causal = a.mask != FA2_MASK_NONE;
 
   TileLoader<DT, D, MODE, BUF> ld(tid);
@@ -589,13 +618,13 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
     if constexpr (!PIPE) compute_s(s_cur, i & 1);
 
     // masks only at the sequence end or on the causal diagonal (wave-uniform)
-    if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
+    if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_diag + w.off))) {
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
         for (int i2 = 0; i2 < 16; ++i2) {
           const int key = k0 + sb * 32 + (i2 >> 2) * 8 + hi * 4 + (i2 & 3);
-          const bool ok = (key < w.Lk) && (!causal || key <= qrow + w.off);
+          const bool ok = (key < w.Lk) && (!causal || key <= qdiag + w.off);
           if (!ok) s_cur[sb][i2] = -INFINITY;
         }
       }
@@ -711,21 +740,24 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
       }
     }
   } else {
-    // Split partials: slot (split, workgroup), row r of the q-block.
+    // Split partials: slot (split, workgroup), row r of the q-block; only
+    // rows the combine reads (r < part_rows, q0 + r < Lq) are written.
     const int64_t slot = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = wave * kWaveRows + l32;
-    if (hi == 0) {
-      float* ml = a.part_ml + (slot * kBM + r) * 2;
-      ml[0] = m_run;
-      ml[1] = l_tot;
+    if (qrow < w.Lq && r < a.part_rows) {
+      if (hi == 0) {
+        float* ml = a.part_ml + (slot * a.part_rows + r) * 2;
+        ml[0] = m_run;
+        ml[1] = l_tot;
+      }
+      float* po = a.part_o + (slot * a.part_rows + r) * D + hi * 4;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
+              (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
     }
-    float* po = a.part_o + (slot * kBM + r) * D + hi * 4;
-#pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
-            (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
   }
 }
 
@@ -742,25 +774,26 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   constexpr int kRowsPerPass = kThreads / kTPR;
   const int S = a.num_splits;
   const int G = a.part_slots;
+  const int R = a.part_rows;
   const int col = (threadIdx.x % kTPR) * 4;
-  for (int r = threadIdx.x / kTPR; r < kBM; r += kRowsPerPass) {
+  for (int r = threadIdx.x / kTPR; r < R; r += kRowsPerPass) {
     const int qrow = q0 + r;
     if (qrow >= w.Lq) break;
     float g = -INFINITY;
     for (int s = 0; s < S; ++s) {
       const int64_t slot = static_cast<int64_t>(s) * G + blockIdx.x;
-      g = fmaxf(g, a.part_ml[(slot * kBM + r) * 2]);
+      g = fmaxf(g, a.part_ml[(slot * R + r) * 2]);
     }
     const float g_use = (g == -INFINITY) ? 0.f : g;
     float lsum = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < S; ++s) {
       const int64_t slot = static_cast<int64_t>(s) * G + blockIdx.x;
-      const float m = a.part_ml[(slot * kBM + r) * 2];
-      const float l = a.part_ml[(slot * kBM + r) * 2 + 1];
+      const float m = a.part_ml[(slot * R + r) * 2];
+      const float l = a.part_ml[(slot * R + r) * 2 + 1];
       const float wgt = fast_exp2(m - g_use);
       lsum += wgt * l;
-      const f32x4 x = *reinterpret_cast<const f32x4*>(a.part_o + (slot * kBM + r) * D + col);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(a.part_o + (slot * R + r) * D + col);
       acc += wgt * x;
     }
     const float inv = 1.f / lsum;
@@ -783,7 +816,7 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
 template <int MODE>
 __device__ __forceinline__ void seq_lens(const KArgs& a, int b, int& Lq, int& Lk) {
   if constexpr (MODE == FA2_LAYOUT_RAGGED) {
-    Lq = a.q_indptr[b + 1] - a.q_indptr[b];
+    Lq = a.pack_m > 0 ? a.q_len : a.q_indptr[b + 1] - a.q_indptr[b];
     Lk = a.kv_indptr[b + 1] - a.kv_indptr[b];
   } else {
     Lq = a.q_len;
@@ -793,9 +826,9 @@ __device__ __forceinline__ void seq_lens(const KArgs& a, int b, int& Lq, int& Lk
   if (Lk < 0) Lk = 0;
 }
 
-__device__ __forceinline__ int block_cost(int mask, int j, int Lq, int Lk) {
+__device__ __forceinline__ int block_cost(int mask, int j, int Lq, int Lk, bool packed) {
   const int off = (mask == FA2_MASK_CAUSAL_BOTTOM_RIGHT) ? (Lk - Lq) : 0;
-  const int e = kv_end_for_block(mask, j * kBM, Lq, Lk, off);
+  const int e = packed ? Lk : kv_end_for_block(mask, j * kBM, Lq, Lk, off);
   const int tiles = (e + kBN - 1) / kBN;
   return tiles < kCostBuckets - 1 ? tiles : kCostBuckets - 1;
 }
@@ -812,7 +845,7 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + kBM - 1) / kBM;
-    for (int j = 0; j < nq; ++j) atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk)], 1);
+    for (int j = 0; j < nq; ++j) atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk, a.pack_m > 0)], 1);
   }
   __syncthreads();
   // Exclusive scan in descending cost order: bucket c starts after all
@@ -847,7 +880,7 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + kBM - 1) / kBM;
     for (int j = 0; j < nq; ++j) {
-      const int pos = atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk)], 1);
+      const int pos = atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk, a.pack_m > 0)], 1);
       if (pos < a.work_ub) work[pos] = make_int2(b, j);
     }
   }

@@ -64,6 +64,8 @@ struct Plan {
   bool pp;          // two-head ping-pong kernel
   int64_t grid_pp;  // its grid: npairs rounded up to kXcds, times Hq / Hkv / 2
   int splits;
+  int part_rows;    // split partials: rows per slot
+  int64_t rows;     // query rows of one unit's sequence (packed: Hq/Hkv * M)
   bool buf;         // K/V byte offsets fit the 31-bit buffer-load path
   uint32_t pool_bytes_k, pool_bytes_v;
   size_t off_work, off_count, off_ml, off_o, total;
@@ -113,9 +115,34 @@ int validate(const fa2_params* p) {
   return FA2_OK;
 }
 
+// Decode / speculative decode: the fa2_fwd checks minus the ragged q_indptr,
+// plus the mask set and the packed q/o row layout (include/fa2.h).
+int validate_decode(const fa2_params* p) {
+  if (!p) return FA2_ERR_NULL_POINTER;
+  if (p->mask == FA2_MASK_CAUSAL_TOP_LEFT) return FA2_ERR_BAD_MASK;
+  if (p->layout == FA2_LAYOUT_RAGGED) {
+    if (!p->kv_indptr) return FA2_ERR_RAGGED_ARGS;
+    fa2_params c = *p;
+    c.q_indptr = p->kv_indptr;  // unused in decode; satisfies the shared check
+    int s = validate(&c);
+    if (s != FA2_OK) return s;
+  } else {
+    int s = validate(p);
+    if (s != FA2_OK) return s;
+  }
+  // unit row r = (head in group) * M + m lives at r * q_ss from the group's
+  // first head (M = 1: the row stride is the head stride)
+  if (p->q_heads / p->kv_heads > 1 &&
+      (p->q_sh != p->q_len * p->q_ss || p->o_sh != p->q_len * p->o_ss))
+    return FA2_ERR_Q_LAYOUT;
+  return FA2_OK;
+}
+
 bool empty_problem(const fa2_params* p) {
   return p->batch == 0 || p->q_len == 0;
 }
+
+int finish_plan(const fa2_params* p, Plan* pl);
 
 int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   const int64_t nqb = cdiv(p->q_len, kBM);
@@ -155,6 +182,14 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     }
   }
   pl->splits = splits;
+  pl->rows = p->q_len;
+  pl->part_rows = kBM;  // the two-head kernel's partial slots assume kBM
+  return finish_plan(p, pl);
+}
+
+// Buffer path and workspace layout, common to both plans.
+int finish_plan(const fa2_params* p, Plan* pl) {
+  const int splits = pl->splits;
   pl->pool_bytes_k = pl->pool_bytes_v = 0;
   pl->buf = buffer_path_ok(p, &pl->pool_bytes_k, &pl->pool_bytes_v);
 
@@ -165,13 +200,51 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   pl->off_count = off;
   if (p->layout != FA2_LAYOUT_DENSE) off += 256;
   pl->off_ml = off;
-  if (splits > 1) off += static_cast<size_t>(splits) * pl->grid_x * kBM * 2 * sizeof(float);
+  if (splits > 1)
+    off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * 2 * sizeof(float);
   off = (off + 255) & ~size_t(255);
   pl->off_o = off;
   if (splits > 1)
-    off += static_cast<size_t>(splits) * pl->grid_x * kBM * p->head_dim * sizeof(float);
+    off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * p->head_dim * sizeof(float);
   pl->total = off;
   return FA2_OK;
+}
+
+// Decode / speculative decode: the Hq/Hkv query heads of a kv head and the M
+// query tokens of a sequence form the rows of one unit (packed-head mode), so
+// a unit streams each K/V row once.  These calls are HBM-bound: the KV sweep
+// is split until the grid holds several workgroups per slot, for balance
+// over unequal sequence lengths.
+int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
+  const int64_t group = p->q_heads / p->kv_heads;
+  pl->rows = group * p->q_len;
+  if (pl->rows > INT32_MAX / 2) return FA2_ERR_TOO_LARGE;
+  const int64_t nqb = cdiv(pl->rows, kBM);
+  pl->work_ub = nqb * p->batch;
+  pl->npairs = pl->work_ub * p->kv_heads;
+  pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds;
+  if (pl->grid_x > INT32_MAX || pl->npairs > INT32_MAX) return FA2_ERR_TOO_LARGE;
+  pl->pp = false;
+  pl->grid_pp = 0;
+  int splits = p->num_splits;
+  if (splits == 0) {
+    const int64_t cus = query_device ? cu_count_current_device() : 256;
+    const int64_t target = 8 * cus;  // workgroups: 4 per slot of 2 per CU
+    // longest possible sequence: N (dense), Tkv (ragged), the pool (paged)
+    const int64_t tiles = cdiv(p->kv_len > 0 ? p->kv_len : INT32_MAX, kBN);
+    splits = 1;
+    if (pl->npairs > 0 && pl->npairs < target) {
+      int64_t sp = cdiv(target, pl->npairs);
+      const int64_t by_tiles = tiles / 2;
+      if (sp > by_tiles) sp = by_tiles;
+      if (sp > FA2_MAX_SPLITS) sp = FA2_MAX_SPLITS;
+      if (sp < 1) sp = 1;
+      splits = static_cast<int>(sp);
+    }
+  }
+  pl->splits = splits;
+  pl->part_rows = static_cast<int>(pl->rows < kBM ? pl->rows : kBM);
+  return finish_plan(p, pl);
 }
 
 template <int DT, int D, int MODE>
@@ -233,7 +306,7 @@ int launch_dim(int d, int mode, const KArgs& a, const Plan& pl, hipStream_t st) 
 
 using namespace fa2;
 
-extern "C" int fa2_abi_version(void) { return 1; }
+extern "C" int fa2_abi_version(void) { return 2; }
 
 extern "C" size_t fa2_params_size(void) { return sizeof(fa2_params); }
 
@@ -253,34 +326,41 @@ extern "C" const char* fa2_strerror(int s) {
     case FA2_ERR_SPLITS: return "num_splits must be in [0, FA2_MAX_SPLITS]";
     case FA2_ERR_HIP: return "a HIP launch or runtime call failed";
     case FA2_ERR_TOO_LARGE: return "a size exceeds the kernels' 32-bit index range";
+    case FA2_ERR_Q_LAYOUT:
+      return "decode: q/o head stride must equal q_len * row stride (contiguous heads)";
     default: return "unknown fa2 status";
   }
 }
 
-extern "C" int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes) {
+namespace fa2 {
+namespace {
+
+int workspace_size(const fa2_params* p, size_t* bytes, bool packed) {
   if (!bytes) return FA2_ERR_NULL_POINTER;
-  int s = validate(p);
+  int s = packed ? validate_decode(p) : validate(p);
   if (s != FA2_OK) return s;
   if (empty_problem(p)) {
     *bytes = 0;
     return FA2_OK;
   }
   Plan pl;
-  s = make_plan(p, &pl, p->num_splits == 0);
+  s = packed ? make_plan_packed(p, &pl, p->num_splits == 0)
+             : make_plan(p, &pl, p->num_splits == 0);
   if (s != FA2_OK) return s;
   *bytes = pl.total;
   return FA2_OK;
 }
 
-extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
-  int s = validate(p);
+int run(const fa2_params* p, void* stream, bool packed) {
+  int s = packed ? validate_decode(p) : validate(p);
   if (s != FA2_OK) return s;
   if (empty_problem(p)) return FA2_OK;
   if (!p->q || !p->k || !p->v || !p->o) return FA2_ERR_NULL_POINTER;
   if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o))
     return FA2_ERR_ALIGNMENT;
   Plan pl;
-  s = make_plan(p, &pl, p->num_splits == 0);
+  s = packed ? make_plan_packed(p, &pl, p->num_splits == 0)
+             : make_plan(p, &pl, p->num_splits == 0);
   if (s != FA2_OK) return s;
   if (pl.total > 0 && (!p->workspace || p->workspace_bytes < pl.total)) return FA2_ERR_WORKSPACE;
 
@@ -302,13 +382,13 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
   a.batch = static_cast<int32_t>(p->batch);
   a.hq = static_cast<int32_t>(p->q_heads);
   a.hkv = static_cast<int32_t>(p->kv_heads);
-  a.q_len = static_cast<int32_t>(p->q_len);
+  a.q_len = static_cast<int32_t>(pl.rows);  // packed: rows of a unit
   a.kv_len = static_cast<int32_t>(p->kv_len);
   a.page_size = static_cast<int32_t>(p->page_size > 0 ? p->page_size : 1);
   a.page_shift = -1;
   for (int s = 0; s < 31; ++s)
     if ((int64_t(1) << s) == a.page_size) a.page_shift = s;
-  a.nqb = static_cast<int32_t>(cdiv(p->q_len, kBM));
+  a.nqb = static_cast<int32_t>(cdiv(pl.rows, kBM));
   a.work_ub = static_cast<int32_t>(pl.work_ub);
   a.npairs = static_cast<int32_t>(pl.npairs);
   a.mask = p->mask;
@@ -324,6 +404,8 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
       p->layout != FA2_LAYOUT_DENSE ? reinterpret_cast<const int32_t*>(ws + pl.off_count) : nullptr;
   a.part_ml = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
   a.part_o = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
+  a.part_rows = pl.part_rows;
+  a.pack_m = packed ? static_cast<int32_t>(p->q_len) : 0;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (p->dtype) {
@@ -332,3 +414,18 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) {
     default: return launch_dim<FA2_DTYPE_F32>(p->head_dim, p->layout, a, pl, st);
   }
 }
+
+}  // namespace
+}  // namespace fa2
+
+extern "C" int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes) {
+  return workspace_size(p, bytes, false);
+}
+
+extern "C" int fa2_fwd(const fa2_params* p, void* stream) { return run(p, stream, false); }
+
+extern "C" int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes) {
+  return workspace_size(p, bytes, true);
+}
+
+extern "C" int fa2_decode_fwd(const fa2_params* p, void* stream) { return run(p, stream, true); }

@@ -385,7 +385,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
   const int split = blockIdx.y;
   const int S = a.num_splits;
 
-  const int kv_end = kv_end_for_block(a.mask, q0, w.Lq, w.Lk, w.off);
+  const int kv_end = kv_end_for_unit(a, q0, w.Lq, w.Lk, w.off);
   const int ntiles = (kv_end + kBN - 1) / kBN;
   const int t_begin = (ntiles * split) / S;
   const int t_end = (ntiles * (split + 1)) / S;
@@ -429,8 +429,15 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
   for (int d = 0; d < DB; ++d) o[d] = (f32x16){};
   float m_run = -INFINITY;
   float l_run = 0.f;
+  // first row of the wave; its rows' smallest diagonal position and this lane's
   const int wq_first = q0 + wave * kWaveRows;
+  const int wq_diag = a.pack_m > 0 ? 0 : wq_first;
+  const int qdiag = diag_row(a, qrow);
   const bool causal = a.mask != FA2_MASK_NONE;
+  // A wave whose 32 rows all lie past the unit's end (small packed-head
+  // units, the last q-block of a sequence) only loads tiles and keeps the
+  // barriers; it computes nothing.
+  const bool active = q0 + wave * kWaveRows < w.Lq;
 
   const DirectLoader<D, MODE, BUF, DT> ld(a, tid);
 
@@ -461,13 +468,14 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         ld.template issue<false>(a, w, k0 + (PIPE ? 2 : 1) * kBN, kbuf[(PIPE ? i : i + 1) & 1]);
       ld.template issue<true>(a, w, k0 + kBN, vbuf[(i + 1) & 1]);
     }
+    if (active) {
     // scores of tile i must exist before they are masked
     if constexpr (!PIPE) compute_s(s_cur, kbuf[i & 1]);
-    if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_first + w.off))) {
+    if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_diag + w.off))) {
       // key = k0 + 4*hi + c with c a compile-time offset per accumulator:
       // visible iff c <= lim (sequence end and, if causal, the diagonal)
       int lim = w.Lk - 1 - k0 - hi * 4;
-      if (causal) lim = min(lim, qrow + w.off - k0 - hi * 4);
+      if (causal) lim = min(lim, qdiag + w.off - k0 - hi * 4);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
@@ -567,6 +575,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
       }
     }
 #endif
+    }  // active
     if constexpr (!kLast) lds_fill_barrier();
   };
   using NotLast = std::integral_constant<bool, false>;
@@ -579,7 +588,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     if (PIPE && T > 1) ld.template issue<false>(a, w, (t_begin + 1) * kBN, kbuf[1]);
     lds_fill_barrier();
     if constexpr (PIPE) {
-      compute_s(sA, kbuf[0]);
+      if (active) compute_s(sA, kbuf[0]);
       // step 0 refills kbuf[0] with K(t0+2): every wave must have finished
       // reading K(t0) first (the barrier also waits for the LDS reads)
       __syncthreads();
@@ -605,20 +614,23 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     store_o_staged<DT, D>(o, inv, lds + wave * OStage<D>::kBytes, a.o, w.o_base, a.o_ss,
                           wq_first, w.Lq, lane);
   } else {
+    // only rows the combine reads (r < part_rows, q0 + r < Lq) are written
     const int64_t slot = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = wave * kWaveRows + l32;
-    if (hi == 0) {
-      float* ml = a.part_ml + (slot * kBM + r) * 2;
-      ml[0] = m_run;
-      ml[1] = l_tot;
+    if (qrow < w.Lq && r < a.part_rows) {
+      if (hi == 0) {
+        float* ml = a.part_ml + (slot * a.part_rows + r) * 2;
+        ml[0] = m_run;
+        ml[1] = l_tot;
+      }
+      float* po = a.part_o + (slot * a.part_rows + r) * D + hi * 4;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
+              (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
     }
-    float* po = a.part_o + (slot * kBM + r) * D + hi * 4;
-#pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
-            (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
   }
 }
 

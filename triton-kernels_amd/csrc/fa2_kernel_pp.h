@@ -471,11 +471,11 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
         const int64_t slot = static_cast<int64_t>(split) * a.part_slots + unit;
         const int rr = wq * kWaveRows + l32;
         if (hi == 0) {
-          float* ml = a.part_ml + (slot * kBM + rr) * 2;
+          float* ml = a.part_ml + (slot * a.part_rows + rr) * 2;
           ml[0] = m_run;
           ml[1] = l_tot;
         }
-        float* po = a.part_o + (slot * kBM + rr) * D + hi * 4;
+        float* po = a.part_o + (slot * a.part_rows + rr) * D + hi * 4;
 #pragma unroll
         for (int d = 0; d < DB; ++d)
 #pragma unroll

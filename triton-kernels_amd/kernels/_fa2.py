@@ -19,9 +19,11 @@ DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 MASK_NONE, MASK_TOP_LEFT, MASK_BOTTOM_RIGHT = 0, 1, 2
 MAX_SPLITS = 64
 
+ABI_VERSION = 2
+
 # Every symbol include/fa2.h declares.
-EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_strerror", "fa2_abi_version",
-           "fa2_params_size")
+EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_strerror", "fa2_decode_workspace_size",
+           "fa2_decode_fwd", "fa2_abi_version", "fa2_params_size")
 
 
 class Fa2Params(ctypes.Structure):
@@ -81,6 +83,11 @@ def lib():
             L.fa2_fwd_workspace_size.restype = ctypes.c_int
             L.fa2_fwd.argtypes = [ctypes.POINTER(Fa2Params), ctypes.c_void_p]
             L.fa2_fwd.restype = ctypes.c_int
+            L.fa2_decode_workspace_size.argtypes = [ctypes.POINTER(Fa2Params),
+                                                    ctypes.POINTER(ctypes.c_size_t)]
+            L.fa2_decode_workspace_size.restype = ctypes.c_int
+            L.fa2_decode_fwd.argtypes = [ctypes.POINTER(Fa2Params), ctypes.c_void_p]
+            L.fa2_decode_fwd.restype = ctypes.c_int
             L.fa2_strerror.argtypes = [ctypes.c_int]
             L.fa2_strerror.restype = ctypes.c_char_p
             L.fa2_abi_version.argtypes = []
@@ -89,6 +96,9 @@ def lib():
             L.fa2_params_size.restype = ctypes.c_size_t
             if L.fa2_params_size() != ctypes.sizeof(Fa2Params):
                 raise RuntimeError("libfa2.so: fa2_params layout mismatch with the binding")
+            if L.fa2_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"libfa2.so: ABI version {L.fa2_abi_version()}, binding "
+                                   f"expects {ABI_VERSION}; rebuild the library")
             _lib = L
     return _lib
 
@@ -100,15 +110,19 @@ class Fa2Error(RuntimeError):
         self.code = code
 
 
-def workspace_size(p: Fa2Params) -> int:
+def workspace_size(p: Fa2Params, decode: bool = False) -> int:
+    """Device workspace bytes of ``fa2_fwd`` (or ``fa2_decode_fwd``) for ``p``."""
     n = ctypes.c_size_t(0)
-    rc = lib().fa2_fwd_workspace_size(ctypes.byref(p), ctypes.byref(n))
+    fn = lib().fa2_decode_workspace_size if decode else lib().fa2_fwd_workspace_size
+    rc = fn(ctypes.byref(p), ctypes.byref(n))
     if rc != 0:
         raise Fa2Error(rc)
     return n.value
 
 
-def forward(p: Fa2Params, stream: int) -> None:
-    rc = lib().fa2_fwd(ctypes.byref(p), ctypes.c_void_p(stream))
+def forward(p: Fa2Params, stream: int, decode: bool = False) -> None:
+    """Enqueue ``fa2_fwd`` (or ``fa2_decode_fwd``) on the HIP stream ``stream``."""
+    fn = lib().fa2_decode_fwd if decode else lib().fa2_fwd
+    rc = fn(ctypes.byref(p), ctypes.c_void_p(stream))
     if rc != 0:
         raise Fa2Error(rc)

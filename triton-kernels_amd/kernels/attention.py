@@ -34,48 +34,7 @@ from __future__ import annotations
 import torch
 
 from . import _fa2
-
-_DTYPES = {
-    torch.float16: _fa2.DTYPE_F16,
-    torch.bfloat16: _fa2.DTYPE_BF16,
-    torch.float32: _fa2.DTYPE_F32,
-}
-SUPPORTED_HEAD_DIMS = (64, 128)
-
-
-def _rows_ok(t: torch.Tensor) -> bool:
-    """Last dim contiguous and every row start 16-byte aligned."""
-    if t.numel() == 0:
-        return True
-    if t.stride(-1) != 1:
-        return False
-    es = t.element_size()
-    if t.data_ptr() % 16:
-        return False
-    return all((s * es) % 16 == 0 for s in t.stride()[:-1])
-
-
-def _prep(t: torch.Tensor) -> torch.Tensor:
-    return t if _rows_ok(t) else t.contiguous()
-
-
-def _strides(t: torch.Tensor):
-    """(batch, head, row) element strides; token-major tensors use (0, head, token)."""
-    if t.dim() == 4:
-        return t.stride(0), t.stride(1), t.stride(2)
-    return 0, t.stride(1), t.stride(0)
-
-
-def _index_tensor(t: torch.Tensor, device) -> torch.Tensor:
-    if t.dtype != torch.int32 or not t.is_contiguous() or t.device != device:
-        t = t.to(device=device, dtype=torch.int32).contiguous()
-    return t
-
-
-def _table(t: torch.Tensor, device) -> torch.Tensor:
-    if t.dtype != torch.int32 or t.stride(-1) != 1 or t.device != device:
-        t = t.to(device=device, dtype=torch.int32).contiguous()
-    return t
+from ._launch import check_dtype_and_dim, enqueue, index_tensor, prep, rows_ok, strides, table
 
 
 def flash_attention_v2(
@@ -161,20 +120,15 @@ def flash_attention_v2(
         layout = _fa2.LAYOUT_PAGED
 
     # --- checks of this build (the reference would fail inside Triton) ----
-    if q.dtype not in _DTYPES:
-        raise TypeError(f"flash_attention_v2: unsupported dtype {q.dtype} "
-                        "(float16, bfloat16, float32)")
-    if head_dim not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"flash_attention_v2: head_dim {head_dim} not supported "
-                         f"(supported: {SUPPORTED_HEAD_DIMS})")
+    check_dtype_and_dim("flash_attention_v2", q.dtype, head_dim)
     if causal_alignment not in ("top_left", "bottom_right"):
         raise ValueError("causal_alignment must be 'top_left' or 'bottom_right'")
 
-    q = _prep(q)
-    k = _prep(k)
-    v = _prep(v)
+    q = prep(q)
+    k = prep(k)
+    v = prep(v)
     out = torch.empty_like(q)
-    if not _rows_ok(out):
+    if not rows_ok(out):
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
     dev = q.device
@@ -182,83 +136,43 @@ def flash_attention_v2(
             (_fa2.MASK_TOP_LEFT if causal_alignment == "top_left" else _fa2.MASK_BOTTOM_RIGHT))
     qi = kvi = kt = vt = None
     if layout == _fa2.LAYOUT_RAGGED:
-        qi = _index_tensor(q_indptr, dev)
-        kvi = _index_tensor(kv_indptr, dev)
+        qi = index_tensor(q_indptr, dev)
+        kvi = index_tensor(kv_indptr, dev)
     elif layout == _fa2.LAYOUT_PAGED:
-        kvi = _index_tensor(kv_indptr, dev)
-        kt = _table(k_block_table, dev)
-        vt = _table(v_block_table, dev)
+        kvi = index_tensor(kv_indptr, dev)
+        kt = table(k_block_table, dev)
+        vt = table(v_block_table, dev)
 
-    # Everything but the pointers depends only on the call signature: build
-    # that part of the parameter block (and its workspace size) once.
-    key = (layout, q.dtype, mask, int(num_splits), dev.index, q.shape, q.stride(), k.shape,
-           k.stride(), v.stride(), out.stride(), batch,
-           None if kt is None else (kt.stride(0), vt.stride(0), int(kv_page_size)))
-    cached = _PLAN_CACHE.get(key)
-    if cached is None:
-        p = _fa2.Fa2Params()
-        p.layout = layout
-        p.dtype = _DTYPES[q.dtype]
-        p.mask = mask
-        p.num_splits = int(num_splits)
-        p.batch = batch
-        p.q_heads = q_heads
-        p.kv_heads = kv_heads
-        p.head_dim = head_dim
-        p.q_len = M
-        p.kv_len = N if layout != _fa2.LAYOUT_PAGED else total_cache
-        p.q_sb, p.q_sh, p.q_ss = _strides(q)
-        p.k_sb, p.k_sh, p.k_ss = _strides(k)
-        p.v_sb, p.v_sh, p.v_ss = _strides(v)
-        p.o_sb, p.o_sh, p.o_ss = _strides(out)
-        if kt is not None:
-            p.k_table_stride, p.v_table_stride = kt.stride(0), vt.stride(0)
-            p.page_size = int(kv_page_size)
-        p.softmax_scale = head_dim ** -0.5
-        # validation needs the layout's pointers; they are overwritten per call
-        p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
-        if qi is not None:
-            p.q_indptr = qi.data_ptr()
-        if kvi is not None:
-            p.kv_indptr = kvi.data_ptr()
-        if kt is not None:
-            p.k_block_table, p.v_block_table = kt.data_ptr(), vt.data_ptr()
-        with torch.cuda.device(dev):
-            ws_bytes = _fa2.workspace_size(p)
-        cached = (bytes(p), ws_bytes)
-        if len(_PLAN_CACHE) >= _PLAN_CACHE_MAX:
-            _PLAN_CACHE.clear()
-        _PLAN_CACHE[key] = cached
-
-    p = _fa2.Fa2Params.from_buffer_copy(cached[0])
-    ws_bytes = cached[1]
-    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
-    if qi is not None:
-        p.q_indptr = qi.data_ptr()
-    if kvi is not None:
-        p.kv_indptr = kvi.data_ptr()
-    if kt is not None:
-        p.k_block_table, p.v_block_table = kt.data_ptr(), vt.data_ptr()
-
-    switch = dev.index != torch.cuda.current_device()
-    if switch:
-        prev = torch.cuda.current_device()
-        torch.cuda.set_device(dev)
-    try:
-        stream = torch.cuda.current_stream(dev)
-        ws = None
-        if ws_bytes:
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-            p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
-        _fa2.forward(p, stream.cuda_stream)
-        if ws is not None:
-            ws.record_stream(stream)
-    finally:
-        if switch:
-            torch.cuda.set_device(prev)
+    enqueue(decode=False, layout=layout, mask=mask, num_splits=num_splits, batch=batch,
+            q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, q_len=M,
+            kv_len=N if layout != _fa2.LAYOUT_PAGED else total_cache,
+            q=q, k=k, v=v, out=out, q_strides=strides(q), o_strides=strides(out),
+            qi=qi, kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size)
     return out
 
 
-# call signature -> (static bytes of the parameter block, workspace bytes)
-_PLAN_CACHE: dict = {}
-_PLAN_CACHE_MAX = 4096
+def flash_attention_v1(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    is_causal: bool = False,
+    q_indptr: torch.Tensor | None = None,
+    kv_indptr: torch.Tensor | None = None,
+    k_block_table: torch.Tensor | None = None,
+    v_block_table: torch.Tensor | None = None,
+    kv_page_size: int | None = None,
+) -> torch.Tensor:
+    """Drop-in for the reference's ``flash_attention_v1``
+    (kernels/attention.py:249-364).
+
+    The reference's v1 has the same signature, the same assertion sequence
+    (:261-330, identical to v2's :762-834), the same layouts, head map,
+    top-left causal mask and softmax scale as v2; it differs only in its
+    Triton schedule (a persistent kernel without split-K).  Both produce the
+    same attention, so v1 is served by the same gfx950 kernels as
+    :func:`flash_attention_v2`, with v1's keyword set.
+    """
+    return flash_attention_v2(q, k, v, is_causal=is_causal, q_indptr=q_indptr,
+                              kv_indptr=kv_indptr, k_block_table=k_block_table,
+                              v_block_table=v_block_table, kv_page_size=kv_page_size)

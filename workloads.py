@@ -16,6 +16,18 @@ c4  paged chunked prefill 32 seqs, ctx ~ U[512,8192], page 16, shuffled pool
                           of ceil(sum/16)+256 pages, q = last 128 tokens
                           (bottom-right causal), Hq32 Hkv8 D128 bf16
 c5  non-causal MQA cross  B4 Hq32 Hkv1 q1024 kv16384 D128 bf16 (+fp32 run)
+
+Decode-side workloads (not BASELINE configs; HBM-bound, reported in GB/s):
+d1  paged decode_attention at the reference decode benchmark's largest
+    point (benchmarks/decode.py:30-44, 170-230): B16, QH8/KVH8, N 8192, D64,
+    page 16, bf16
+d2  paged decode_attention, serving shape: 64 seqs, ctx ~ U[512,8192],
+    shuffled pool of ceil(sum/16)+256 pages, Hq32 Hkv8 D128 bf16
+s1  paged speculative_decode_attention, causal, M 8 drafts, at the
+    reference benchmark's shape (benchmarks/speculative_decode.py:29-50):
+    B16, QH8/KVH8, N 8192 + 8 drafts, D64, page 16, bf16
+s2  paged speculative_decode_attention, causal, M 8, serving shape of d2
+    (context + 8 drafts per sequence), Hq32 Hkv8 D128 bf16
 """
 
 from __future__ import annotations
@@ -25,7 +37,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-CONFIGS = ("c1", "c2", "c3", "c4", "c5")
+CONFIGS = ("c1", "c2", "c3", "c4", "c5", "d1", "d2", "s1", "s2")
 PAGE = 16
 
 
@@ -49,11 +61,17 @@ class Workload:
     q_heads: int = 0
     kv_heads: int = 0
     head_dim: int = 0
+    kind: str = "prefill"       # prefill (flash_attention_v2) | decode | speculative
 
     def kwargs(self) -> dict:
-        kw = dict(is_causal=self.is_causal)
-        if self.causal_alignment != "top_left":
-            kw["causal_alignment"] = self.causal_alignment
+        if self.kind == "decode":
+            kw = {}
+        elif self.kind == "speculative":
+            kw = dict(causal=self.is_causal)
+        else:
+            kw = dict(is_causal=self.is_causal)
+            if self.causal_alignment != "top_left":
+                kw["causal_alignment"] = self.causal_alignment
         for n in ("q_indptr", "kv_indptr", "k_block_table", "v_block_table", "kv_page_size"):
             val = getattr(self, n)
             if val is not None:
@@ -95,7 +113,10 @@ def flops(w: Workload) -> float:
 def hbm_bytes(w: Workload) -> float:
     """Q and O once at Hq, K and V once at Hkv (tokens actually attended)."""
     es = torch.tensor([], dtype=w.dtype).element_size()
-    sq = sum(w.q_lens) if w.layout == "ragged" else w.q.shape[0] * w.q.shape[2]
+    if w.kind != "prefill":
+        sq = sum(w.q_lens)
+    else:
+        sq = sum(w.q_lens) if w.layout == "ragged" else w.q.shape[0] * w.q.shape[2]
     sk = sum(w.kv_lens)
     return es * w.head_dim * (2 * sq * w.q_heads + 2 * sk * w.kv_heads)
 
@@ -241,7 +262,47 @@ def make(name: str, dtype: torch.dtype | None = None, seed: int = 0,
         v = _randn(gen, (B, Hkv, N, D), dt)
         return Workload("c5", "dense", dt, q, k, v, False, q_lens=[M] * B, kv_lens=[N] * B,
                         q_heads=Hq, kv_heads=Hkv, head_dim=D)
+    if name in ("d1", "d2", "s1", "s2"):
+        return _make_decode(name, dtype or torch.bfloat16, gen)
     raise KeyError(name)
+
+
+def _make_decode(name, dt, gen) -> Workload:
+    """Paged decode / speculative-decode workloads (see the module docstring)."""
+    spec = name.startswith("s")
+    M = 8 if spec else 1
+    if name in ("d1", "s1"):
+        B, Hq, Hkv, D = 16, 8, 8, 64
+        ctx = [8192] * B
+    else:
+        B, Hq, Hkv, D = 64, 32, 8, 128
+        ctx = torch.randint(512, 8193, (B,), generator=gen).tolist()
+    lens = [c + (M if spec else 0) for c in ctx]  # drafts are the last M keys
+    nb = [(n + PAGE - 1) // PAGE for n in lens]
+    pool = sum(nb) + (256 if name in ("d2", "s2") else 0)
+    kc = _randn(gen, (pool * PAGE, Hkv, D), dt)
+    vc = _randn(gen, (pool * PAGE, Hkv, D), dt)
+    if name in ("d2", "s2"):
+        kperm = torch.randperm(pool, generator=gen)
+        vperm = torch.randperm(pool, generator=gen)
+        pad = -1
+    else:  # the reference benchmark's allocate_paged_cache: pages in order, padding 0
+        kperm = vperm = torch.arange(pool)
+        pad = 0
+    kt = torch.full((B, max(nb)), pad, dtype=torch.int32)
+    vt = torch.full((B, max(nb)), pad, dtype=torch.int32)
+    cur = 0
+    for b in range(B):
+        kt[b, : nb[b]] = kperm[cur: cur + nb[b]].to(torch.int32)
+        vt[b, : nb[b]] = vperm[cur: cur + nb[b]].to(torch.int32)
+        cur += nb[b]
+    q = _randn(gen, (B, Hq, M, D) if spec else (B, Hq, D), dt)
+    return Workload(name, "paged", dt, q, kc, vc, spec,
+                    causal_alignment="bottom_right" if spec else "top_left",
+                    kv_indptr=torch.tensor(lens, dtype=torch.int32), k_block_table=kt,
+                    v_block_table=vt, kv_page_size=PAGE, q_lens=[M] * B, kv_lens=lens,
+                    q_heads=Hq, kv_heads=Hkv, head_dim=D,
+                    kind="speculative" if spec else "decode")
 
 
 def sequences(w: Workload):
@@ -260,7 +321,8 @@ def sequences(w: Workload):
             ks.append(w.k[ka:kb])
             vs.append(w.v[ka:kb])
         else:
-            qs.append(w.q[b].transpose(0, 1))
+            qb = w.q[b].unsqueeze(1) if w.kind == "decode" else w.q[b]
+            qs.append(qb.transpose(0, 1))
             ks.append(_gather_one(w.k, w.k_block_table[b], w.kv_lens[b], w.kv_page_size))
             vs.append(_gather_one(w.v, w.v_block_table[b], w.kv_lens[b], w.kv_page_size))
     return qs, ks, vs
