@@ -107,6 +107,7 @@ struct KArgs {
   // then the unit's row count Hq/Hkv * pack_m.  Causal is bottom-right per
   // draft position: row r sees key j iff j <= Lk - pack_m + r % pack_m.
   int32_t pack_m;
+  int32_t block_rows;   // unit rows per q-block of the launched kernel (kBM; decode kernel 64)
 };
 
 // ---------------------------------------------------------------------------
@@ -769,7 +770,7 @@ template <int DT, int D, int MODE>
 __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   const Work w = decode_work<MODE>(a, blockIdx.x);
   if (!w.valid) return;
-  const int q0 = w.qblk * kBM;
+  const int q0 = w.qblk * a.block_rows;
   constexpr int kTPR = D / 4;  // threads per row, 4 floats each
   constexpr int kRowsPerPass = kThreads / kTPR;
   const int S = a.num_splits;
@@ -844,7 +845,7 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
   for (int b = tid; b < a.batch; b += kPlanThreads) {
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
-    const int nq = (Lq + kBM - 1) / kBM;
+    const int nq = (Lq + a.block_rows - 1) / a.block_rows;
     for (int j = 0; j < nq; ++j) atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk, a.pack_m > 0)], 1);
   }
   __syncthreads();
@@ -878,7 +879,7 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
   for (int b = tid; b < a.batch; b += kPlanThreads) {
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
-    const int nq = (Lq + kBM - 1) / kBM;
+    const int nq = (Lq + a.block_rows - 1) / a.block_rows;
     for (int j = 0; j < nq; ++j) {
       const int pos = atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk, a.pack_m > 0)], 1);
       if (pos < a.work_ub) work[pos] = make_int2(b, j);

@@ -17,6 +17,7 @@
 #include "fa2_device.h"
 #include "fa2_kernel_lds.h"
 #include "fa2_kernel_pp.h"
+#include "fa2_kernel_decode.h"
 
 // 1: fp16/bf16 with an even number of query heads per kv head run the
 // two-head ping-pong kernel; 0: always the one-head kernel.
@@ -66,6 +67,8 @@ struct Plan {
   int splits;
   int part_rows;    // split partials: rows per slot
   int64_t rows;     // query rows of one unit's sequence (packed: Hq/Hkv * M)
+  int block_rows;   // rows per q-block of the launched kernel
+  bool dec;         // packed fp16/bf16: the decode kernel
   bool buf;         // K/V byte offsets fit the 31-bit buffer-load path
   uint32_t pool_bytes_k, pool_bytes_v;
   size_t off_work, off_count, off_ml, off_o, total;
@@ -183,6 +186,8 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   }
   pl->splits = splits;
   pl->rows = p->q_len;
+  pl->block_rows = kBM;
+  pl->dec = false;
   pl->part_rows = kBM;  // the two-head kernel's partial slots assume kBM
   return finish_plan(p, pl);
 }
@@ -219,7 +224,11 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   const int64_t group = p->q_heads / p->kv_heads;
   pl->rows = group * p->q_len;
   if (pl->rows > INT32_MAX / 2) return FA2_ERR_TOO_LARGE;
-  const int64_t nqb = cdiv(pl->rows, kBM);
+  // fp16/bf16: the decode kernel (64-row blocks, one workgroup per CU);
+  // fp32: the register-staged kernel (128-row blocks, two per CU)
+  pl->dec = p->dtype != FA2_DTYPE_F32;
+  pl->block_rows = pl->dec ? kDecRows : kBM;
+  const int64_t nqb = cdiv(pl->rows, pl->block_rows);
   pl->work_ub = nqb * p->batch;
   pl->npairs = pl->work_ub * p->kv_heads;
   pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds;
@@ -229,13 +238,15 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   int splits = p->num_splits;
   if (splits == 0) {
     const int64_t cus = query_device ? cu_count_current_device() : 256;
-    const int64_t target = 8 * cus;  // workgroups: 4 per slot of 2 per CU
+    // the decode kernel holds a CU alone: one workgroup per CU (measured on
+    // MI355X: 128 units of 128 tiles run best at 2 splits, 512 units at 1)
+    const int64_t target = cus;
     // longest possible sequence: N (dense), Tkv (ragged), the pool (paged)
     const int64_t tiles = cdiv(p->kv_len > 0 ? p->kv_len : INT32_MAX, kBN);
     splits = 1;
     if (pl->npairs > 0 && pl->npairs < target) {
       int64_t sp = cdiv(target, pl->npairs);
-      const int64_t by_tiles = tiles / 2;
+      const int64_t by_tiles = tiles / 8;  // keep the LDS ring in steady state
       if (sp > by_tiles) sp = by_tiles;
       if (sp > FA2_MAX_SPLITS) sp = FA2_MAX_SPLITS;
       if (sp < 1) sp = 1;
@@ -243,7 +254,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
     }
   }
   pl->splits = splits;
-  pl->part_rows = static_cast<int>(pl->rows < kBM ? pl->rows : kBM);
+  pl->part_rows = static_cast<int>(pl->rows < pl->block_rows ? pl->rows : pl->block_rows);
   return finish_plan(p, pl);
 }
 
@@ -254,6 +265,20 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
                        const_cast<int2*>(a.work), const_cast<int32_t*>(a.work_count));
   }
   const dim3 grid(pl.grid_x, pl.splits);
+  if constexpr (DT != FA2_DTYPE_F32) {
+    if (pl.dec) {
+      if (pl.buf)
+        hipLaunchKernelGGL((fa2_decode_kernel<DT, D, MODE, true>), grid, dim3(kDecThreads), 0, st,
+                           a);
+      else
+        hipLaunchKernelGGL((fa2_decode_kernel<DT, D, MODE, false>), grid, dim3(kDecThreads), 0, st,
+                           a);
+      if (pl.splits > 1)
+        hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), dim3(pl.grid_x), dim3(kThreads), 0,
+                           st, a);
+      return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
+    }
+  }
   if constexpr (DT == FA2_DTYPE_F32) {
     if (pl.buf)
       hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
@@ -388,7 +413,8 @@ int run(const fa2_params* p, void* stream, bool packed) {
   a.page_shift = -1;
   for (int s = 0; s < 31; ++s)
     if ((int64_t(1) << s) == a.page_size) a.page_shift = s;
-  a.nqb = static_cast<int32_t>(cdiv(pl.rows, kBM));
+  a.nqb = static_cast<int32_t>(cdiv(pl.rows, pl.block_rows));
+  a.block_rows = pl.block_rows;
   a.work_ub = static_cast<int32_t>(pl.work_ub);
   a.npairs = static_cast<int32_t>(pl.npairs);
   a.mask = p->mask;

@@ -171,6 +171,49 @@ struct DirectLoader {
     return scalar_load_i32(table + idx) * a.page_size + poff;
   }
 
+  // Callers that read the table ahead of its use (decode producers): true
+  // when one table entry serves each wave's kSpan rows of a tile.
+  __device__ __forceinline__ static bool uniform_pages(const KArgs& a) {
+    return MODE == FA2_LAYOUT_PAGED && BUF && a.page_size % kSpan == 0;
+  }
+
+  // Block-table entry of this wave's first row of the tile at k0, through a
+  // constant-address-space load: a scalar load whose wait the compiler
+  // places at the first use, so it can be issued a tile ahead (the entry is
+  // returned raw; issue_at turns it into a row).
+  __device__ __forceinline__ int prefetch_page(const KArgs& a, const Work& w, int k0,
+                                               bool is_v) const {
+    typedef __attribute__((address_space(4))) const int32_t const_i32_t;
+    const int n = min(k0 + wave * kSpan, w.Lk - 1);
+    const int pidx = a.page_shift >= 0 ? (n >> a.page_shift) : n / a.page_size;
+    const int32_t* tbl = is_v ? a.v_table : a.k_table;
+    const int64_t ts = is_v ? a.v_table_stride : a.k_table_stride;
+    const int idx = __builtin_amdgcn_readfirstlane(static_cast<int>(w.b * ts + pidx));
+    return ((const_i32_t*)tbl)[idx];
+  }
+
+  // issue<IS_V> for uniform_pages() with the table entry from prefetch_page.
+  template <bool IS_V>
+  __device__ __forceinline__ void issue_at(const KArgs& a, const Work& w, int k0, void* dst,
+                                           int page) const {
+    const void* src = IS_V ? a.v : a.k;
+    const int64_t base = IS_V ? w.v_base : w.k_base;
+    const uint32_t ldst = lds_addr_of(dst) + wave * kInstr * 1024;
+    const uint32_t rsb = static_cast<uint32_t>((IS_V ? a.v_ss : a.k_ss) * kEB);
+    const u32x4 rsrc = rsrc_words(static_cast<const char*>(src) + base * kEB,
+                                  IS_V ? a.pool_bytes_v : a.pool_bytes_k);
+    const int n0 = k0 + wave * kSpan;
+    const int nc = min(n0, w.Lk - 1);
+    const int poff = a.page_shift >= 0 ? (nc & (a.page_size - 1)) : nc % a.page_size;
+    const uint32_t urow =
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(page * a.page_size + poff));
+#pragma unroll
+    for (int j = 0; j < kInstr; ++j) {
+      const uint32_t off = (urow + j * kRPI) * rsb + (IS_V ? vvo[j] : kvo[j]);
+      dma_buffer_x4(rsrc, ldst + j * 1024, n0 + j * kRPI + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+    }
+  }
+
   __device__ __forceinline__ static int paged_row(const int32_t* table, int64_t tstride, int b,
                                                   int n, int page) {
     const int pg = table[b * tstride + n / page];
