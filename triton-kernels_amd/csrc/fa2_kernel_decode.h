@@ -12,11 +12,12 @@
 //     kv head, split);
 //   * waves 4-7 (producers) only issue the direct-to-LDS DMAs of each 64-key
 //     tile (DirectLoader, the prefill kernel's swizzled layout, a quarter of
-//     the tile each), keeping kStages - 1 tiles (96 KiB at D = 128, 112 KiB
-//     at D = 64) in flight; after its part of tile j has landed
+//     the tile each; at D = 64 a tile is two 64-key sub-tiles, 128 keys),
+//     keeping kStages - 1 tiles (96 KiB) in flight; after its part of tile j
+//     has landed
 //     (s_waitcnt vmcnt) a producer adds 1 to ready[j % kStages];
 //   * waves 0-3 (consumers) wait for ready[] to count all four parts, compute
-//     keys [32 (w & 1), +32) of the tile for row chunk w >> 1 on
+//     keys [32 (w & 1), +32) of each 64-key sub-tile for row chunk w >> 1 on
 //     v_mfma_f32_32x32x16 (S^T = K Q^T, O^T = V^T P^T, the prefill kernel's
 //     fragment layouts), then add 1 to done[j % kStages]; a producer reuses a
 //     slot once done[] counts every active consumer;
@@ -37,14 +38,20 @@ constexpr int kDecWaves = 8;      // 4 consumers + 4 producers
 constexpr int kDecThreads = 64 * kDecWaves;
 constexpr int kDecSpinCap = 1 << 16;  // ~5 ms of polling; real waits are microseconds
 
+// A ring slot holds kSub 64-key sub-tiles of K, then the same of V, so that
+// one slot is 32 KiB at both head dims (the per-slot handshake costs the
+// same whatever the slot size).
 template <int D>
 struct DecGeo {
   using G = SwzGeo<D>;
-  static constexpr int kStages = D == 128 ? 4 : 8;
-  static constexpr int kSlot = 2 * G::kTileBytes;  // K then V of one 64-key tile
+  static constexpr int kSub = D == 128 ? 1 : 2;
+  static constexpr int kKeys = kSub * kBN;              // keys per slot
+  static constexpr int kStages = 4;
+  static constexpr int kHalf = kSub * G::kTileBytes;    // K (or V) part of a slot
+  static constexpr int kSlot = 2 * kHalf;
   static constexpr int kLdsBytes = kStages * kSlot;
-  // DMA instructions one producer wave issues per tile (K and V)
-  static constexpr int kInstrPerTile = 2 * (G::kNC / 4);
+  // DMA instructions one producer wave issues per slot (K and V)
+  static constexpr int kInstrPerTile = kSub * 2 * (G::kNC / 4);
 };
 
 // s_waitcnt vmcnt(n * IPT) for a wave-uniform n in [0, NS - 1]; the count
@@ -116,7 +123,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
   const int split = blockIdx.y;
   const int S = a.num_splits;
 
-  const int ntiles = (w.Lk + kBN - 1) / kBN;
+  constexpr int SUB = DG::kSub;
+  const int ntiles = (w.Lk + DG::kKeys - 1) / DG::kKeys;
   const int t_begin = (ntiles * split) / S;
   const int T = (ntiles * (split + 1)) / S - t_begin;
 
@@ -145,27 +153,49 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
     // paged caches with whole pages per wave and tile: the block-table
     // entries of tile i + 1 are read while tile i is issued
     const bool pre = Ld::uniform_pages(a);
-    int rk = 0, rv = 0;
+    int rk[SUB], rv[SUB];
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) rk[u] = rv[u] = 0;
     if (pre && T > 0) {
-      rk = ld.prefetch_page(a, w, t_begin * kBN, false);
-      rv = ld.prefetch_page(a, w, t_begin * kBN, true);
+#pragma unroll
+      for (int u = 0; u < SUB; ++u) {
+        rk[u] = ld.prefetch_page(a, w, t_begin * DG::kKeys + u * kBN, false);
+        rv[u] = ld.prefetch_page(a, w, t_begin * DG::kKeys + u * kBN, true);
+      }
     }
     for (int i = 0; i < T; ++i) {
       // slot i % NS held tile i - NS: wait until every active consumer is done
       if (i >= NS) lds_wait_geq(done + i % NS, nact * (i / NS));
       char* sl = slot(i);
-      const int k0 = (t_begin + i) * kBN;
+      const int k0 = (t_begin + i) * DG::kKeys;
       if (pre) {
-        const int ck = rk, cv = rv;
-        if (i + 1 < T) {
-          rk = ld.prefetch_page(a, w, k0 + kBN, false);
-          rv = ld.prefetch_page(a, w, k0 + kBN, true);
+        int ck[SUB], cv[SUB];
+#pragma unroll
+        for (int u = 0; u < SUB; ++u) {
+          ck[u] = rk[u];
+          cv[u] = rv[u];
         }
-        ld.template issue_at<false>(a, w, k0, sl, ck);
-        ld.template issue_at<true>(a, w, k0, sl + G::kTileBytes, cv);
+        if (i + 1 < T) {
+#pragma unroll
+          for (int u = 0; u < SUB; ++u) {
+            rk[u] = ld.prefetch_page(a, w, k0 + DG::kKeys + u * kBN, false);
+            rv[u] = ld.prefetch_page(a, w, k0 + DG::kKeys + u * kBN, true);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < SUB; ++u)
+          ld.template issue_at<false>(a, w, k0 + u * kBN, sl + u * G::kTileBytes, ck[u]);
+#pragma unroll
+        for (int u = 0; u < SUB; ++u)
+          ld.template issue_at<true>(a, w, k0 + u * kBN, sl + DG::kHalf + u * G::kTileBytes,
+                                     cv[u]);
       } else {
-        ld.template issue<false>(a, w, k0, sl);
-        ld.template issue<true>(a, w, k0, sl + G::kTileBytes);
+#pragma unroll
+        for (int u = 0; u < SUB; ++u)
+          ld.template issue<false>(a, w, k0 + u * kBN, sl + u * G::kTileBytes);
+#pragma unroll
+        for (int u = 0; u < SUB; ++u)
+          ld.template issue<true>(a, w, k0 + u * kBN, sl + DG::kHalf + u * G::kTileBytes);
       }
       if (i >= L) {  // tile i - L has landed once only the L newer tiles are in flight
         wait_tiles_after<IPT, NS>(L);
@@ -209,9 +239,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
 
     for (int i = 0; i < T; ++i) {
       lds_wait_geq(ready + i % NS, 4 * (i / NS + 1));  // all four producers' parts
-      const lds_char_t* kl = to_lds(slot(i));
-      const lds_char_t* vl = kl + G::kTileBytes;
-      const int k0 = (t_begin + i) * kBN;
+#pragma unroll
+      for (int u = 0; u < SUB; ++u) {
+      const lds_char_t* kl = to_lds(slot(i)) + u * G::kTileBytes;
+      const lds_char_t* vl = to_lds(slot(i)) + DG::kHalf + u * G::kTileBytes;
+      const int k0 = (t_begin + i) * DG::kKeys + u * kBN;
 
       f32x16 s = (f32x16){};
 #pragma unroll
@@ -280,6 +312,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
           o[d] = mma32<BF>((u32x4){l2[0], l2[1], h2[0], h2[1]}, pf[c], o[d]);
         }
       }
+      }  // sub-tiles
       lds_signal(done + i % NS, lane);  // this wave's reads of the slot are complete
     }
   }

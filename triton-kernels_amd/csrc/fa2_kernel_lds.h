@@ -270,7 +270,8 @@ struct DirectLoader {
           }
         }
       } else {
-        const uint32_t lim = static_cast<uint32_t>(w.Lk - k0) * rsb;
+        // rows past the sequence read as zeros (a tile wholly past it: none)
+        const uint32_t lim = static_cast<uint32_t>(max(w.Lk - k0, 0)) * rsb;
         const u32x4 rsrc = rsrc_words(
             static_cast<const char*>(src) + (base + static_cast<int64_t>(k0) * rs) * kEB, lim);
 #pragma unroll
