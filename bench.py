@@ -51,6 +51,7 @@ DESCR = {
     "d2": "d2 paged decode 64 seqs ctx~U[512,8192] page16 Hq32 Hkv8 D128",
     "s1": "s1 paged speculative decode causal M8 B16 QH8 KVH8 N8192+8 D64 page16",
     "s2": "s2 paged speculative decode causal M8 64 seqs ctx~U[512,8192]+8 page16 Hq32 Hkv8 D128",
+    "a1": "a1 paged_kv_append of c4's context (140567 rows x Hkv8 x D128) into shuffled pools",
     "c1": "c1 dense causal MHA B1 H8 L512 D64",
     "c2": "c2 dense causal GQA B2 Hq32 Hkv8 L2048 D128",
     "c3": "c3 ragged causal self 16 seqs L~U[128,4096] Hq32 Hkv8 D128",
@@ -188,11 +189,18 @@ def main(argv=None):
     nbytes = W.hbm_bytes(w)
     flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if args.flush else None
 
-    fn = {"prefill": flash_attention_v2, "decode": decode_attention,
-          "speculative": speculative_decode_attention}[w.kind]
+    if w.kind == "append":
+        from kernels.paged_cache import paged_kv_append as fn
 
-    def step():
-        return fn(w.q, w.k, w.v, **kw)
+        def step():
+            return fn(w.k, w.v, w.k_block_table, w.v_block_table, w.k_new, w.v_new,
+                      w.new_indptr, w.kv_page_size)
+    else:
+        fn = {"prefill": flash_attention_v2, "decode": decode_attention,
+              "speculative": speculative_decode_attention}[w.kind]
+
+        def step():
+            return fn(w.q, w.k, w.v, **kw)
 
     print(f"bench: {DESCR[args.config]} {DTYPE_NAME[w.dtype]} warmup={args.warmup} "
           f"steps={args.steps}", file=sys.stderr, flush=True)
@@ -273,7 +281,7 @@ def main(argv=None):
         },
         "cpu_baseline": None,
     }
-    if not args.no_cpu:
+    if not args.no_cpu and w.kind != "append":
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(w_cpu, args.cpu_budget)
     print(json.dumps(line), flush=True)

@@ -180,6 +180,56 @@ int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes);
  * reported before any launch.  No allocation, no host synchronisation. */
 int fa2_decode_fwd(const fa2_params* p, void* stream);
 
+/* ---- paged KV-cache writer -------------------------------------------------
+ *
+ * Writes new K/V rows into the paged caches the attention entry points read.
+ * The reference has no kernel for this step: its paged layout is built on
+ * the host by tests/test_attention.py:101-134 (`allocate_paged_cache`, pages
+ * in sequence order, table padding 0), tests/test_decode.py:93-130 and
+ * benchmarks/attention.py:351-431 (`build_paged_cache`, padding -1).  The
+ * format is theirs: a cache is [num_pages * page_size, kv_heads, head_dim],
+ * and logical row n of sequence b lives at row
+ * table[b][n / page_size] * page_size + n % page_size.
+ *
+ * Sequence b's new rows k_new[new_indptr[b] + j] (j < new_indptr[b+1] -
+ * new_indptr[b]) go to logical positions start_pos[b] + j (start_pos NULL:
+ * 0, i.e. building a cache; the current lengths: appending decode tokens).
+ * Rows whose logical page is >= table_width, or whose table entry is outside
+ * [0, num_pages), are skipped (never written).  v_new, v_cache and
+ * v_block_table may all be NULL: then only K is written.  Strides are in ELEMENTS;
+ * head_dim must be contiguous and rows 16-byte aligned; k_new/v_new share
+ * strides, as do the two caches.  No allocation, no host synchronisation. */
+typedef struct fa2_kv_append_params {
+  int32_t dtype;            /* enum fa2_dtype of caches and new rows          */
+  int32_t reserved0;
+  int64_t batch;            /* B                                               */
+  int64_t kv_heads;         /* H                                               */
+  int64_t head_dim;         /* D                                               */
+  int64_t num_rows;         /* rows of k_new / v_new (= new_indptr[B])         */
+  int64_t page_size;        /* P (tokens per page)                             */
+  int64_t num_pages;        /* pages of each cache (cache rows / P)            */
+  int64_t table_width;      /* columns of the block tables                     */
+  int64_t k_table_stride;   /* row strides of the block tables (elements)      */
+  int64_t v_table_stride;
+  int64_t new_ts, new_hs;   /* element strides (row, head) of k_new / v_new    */
+  int64_t cache_ts, cache_hs; /* element strides (row, head) of the caches     */
+  const void* k_new;
+  const void* v_new;
+  void* k_cache;
+  void* v_cache;
+  const int32_t* new_indptr;    /* [B+1] prefix sums over the new rows         */
+  const int32_t* start_pos;     /* [B] first logical position, or NULL (0)     */
+  const int32_t* k_block_table; /* [B, table_width]                            */
+  const int32_t* v_block_table;
+} fa2_kv_append_params;
+
+/* Validate `p` and enqueue the writes on `stream`.  Returns FA2_OK or an
+ * error code (before any launch). */
+int fa2_kv_append(const fa2_kv_append_params* p, void* stream);
+
+/* sizeof(fa2_kv_append_params) as compiled into the library (binding check). */
+size_t fa2_kv_append_params_size(void);
+
 /* Version of this ABI (bumped on any change to fa2_params).  No counterpart
  * in the reference: lets a binding refuse a library it was not written for. */
 int fa2_abi_version(void);

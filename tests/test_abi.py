@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layout_matches():
     assert _fa2.lib().fa2_params_size() == ctypes.sizeof(_fa2.Fa2Params)
-    assert _fa2.lib().fa2_abi_version() == _fa2.ABI_VERSION == 2
+    assert _fa2.lib().fa2_abi_version() == _fa2.ABI_VERSION == 3
 
 
 def test_strerror_for_every_code():
@@ -142,8 +142,9 @@ def test_product_path_does_not_import_the_oracle():
 # ---- decode / speculative decode entry points ------------------------------
 
 def decode_params(M=1, **kw):
-    """q/o [B=2, Hq=8, M, D=128] over a dense K/V [2, 2, 300, 128]."""
-    p = dense_params(mask=0, num_splits=0, q_len=M)
+    """q/o [B=2, Hq=8, M, D=128] over a dense K/V [2, 2, 4096, 128]."""
+    p = dense_params(mask=0, num_splits=0, q_len=M, kv_len=4096, k_sb=2 * 4096 * 128,
+                     k_sh=4096 * 128, v_sb=2 * 4096 * 128, v_sh=4096 * 128)
     p.q_sb, p.q_sh, p.q_ss = 8 * M * 128, M * 128, 128 if M > 1 else M * 128
     p.o_sb, p.o_sh, p.o_ss = p.q_sb, p.q_sh, p.q_ss
     for k, v in kw.items():
@@ -162,7 +163,7 @@ def rc_dec(p):
 def test_decode_workspace_ok(M):
     r1, _, n = rc_dec(decode_params(M, q=0))
     assert r1 == 0
-    # 8 query heads share 2 kv heads: units = B * Hkv = 4, so the KV sweep is split
+    # 8 query heads share 2 kv heads: 4 units of 64 key tiles, so the KV sweep is split
     assert n > 0
 
 

@@ -18,6 +18,7 @@
 #include "fa2_kernel_lds.h"
 #include "fa2_kernel_pp.h"
 #include "fa2_kernel_decode.h"
+#include "fa2_kv_append.h"
 
 // 1: fp16/bf16 with an even number of query heads per kv head run the
 // two-head ping-pong kernel; 0: always the one-head kernel.
@@ -331,7 +332,7 @@ int launch_dim(int d, int mode, const KArgs& a, const Plan& pl, hipStream_t st) 
 
 using namespace fa2;
 
-extern "C" int fa2_abi_version(void) { return 2; }
+extern "C" int fa2_abi_version(void) { return 3; }
 
 extern "C" size_t fa2_params_size(void) { return sizeof(fa2_params); }
 
@@ -455,3 +456,61 @@ extern "C" int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes) {
 }
 
 extern "C" int fa2_decode_fwd(const fa2_params* p, void* stream) { return run(p, stream, true); }
+
+extern "C" size_t fa2_kv_append_params_size(void) { return sizeof(fa2_kv_append_params); }
+
+extern "C" int fa2_kv_append(const fa2_kv_append_params* p, void* stream) {
+  if (!p) return FA2_ERR_NULL_POINTER;
+  if (p->dtype < FA2_DTYPE_F16 || p->dtype > FA2_DTYPE_F32) return FA2_ERR_BAD_DTYPE;
+  if (p->batch < 0 || p->kv_heads <= 0 || p->head_dim <= 0 || p->num_rows < 0 ||
+      p->page_size <= 0 || p->num_pages < 0 || p->table_width < 0 || p->k_table_stride < 0 ||
+      p->v_table_stride < 0)
+    return FA2_ERR_BAD_SHAPE;
+  if (p->batch == 0 || p->num_rows == 0) return FA2_OK;
+  // V is optional (all three V pointers null: only K is written)
+  const bool has_v = p->v_new || p->v_cache || p->v_block_table;
+  if (!p->k_new || !p->k_cache || !p->new_indptr || !p->k_block_table ||
+      (has_v && (!p->v_new || !p->v_cache || !p->v_block_table)))
+    return FA2_ERR_NULL_POINTER;
+  const int64_t eb = elt_bytes(p->dtype);
+  const int64_t row_bytes = p->head_dim * eb;
+  if (row_bytes % 16) return FA2_ERR_ALIGNMENT;
+  const int64_t strides[] = {p->new_ts, p->new_hs, p->cache_ts, p->cache_hs};
+  for (int64_t st : strides)
+    if (!stride_ok(st, static_cast<int>(eb))) return FA2_ERR_ALIGNMENT;
+  if (!aligned16(p->k_new) || !aligned16(p->k_cache) ||
+      (has_v && (!aligned16(p->v_new) || !aligned16(p->v_cache))))
+    return FA2_ERR_ALIGNMENT;
+  const int64_t lim = INT32_MAX / 2;
+  if (p->batch > lim || p->num_rows > lim || p->page_size > lim || p->table_width > lim ||
+      p->kv_heads * (row_bytes / 16) > lim)
+    return FA2_ERR_TOO_LARGE;
+  AppendArgs a{};
+  a.k_new = static_cast<const char*>(p->k_new);
+  a.v_new = static_cast<const char*>(p->v_new);
+  a.k_cache = static_cast<char*>(p->k_cache);
+  a.v_cache = static_cast<char*>(p->v_cache);
+  a.indptr = p->new_indptr;
+  a.start = p->start_pos;
+  a.k_table = p->k_block_table;
+  a.v_table = p->v_block_table;
+  a.new_ts = p->new_ts * eb;
+  a.new_hs = p->new_hs * eb;
+  a.cache_ts = p->cache_ts * eb;
+  a.cache_hs = p->cache_hs * eb;
+  a.k_table_stride = p->k_table_stride;
+  a.v_table_stride = p->v_table_stride;
+  a.num_pages = p->num_pages;
+  a.batch = static_cast<int32_t>(p->batch);
+  a.heads = static_cast<int32_t>(p->kv_heads);
+  a.head_chunks = static_cast<int32_t>(row_bytes / 16);
+  a.row_chunks = static_cast<int32_t>(p->kv_heads * (row_bytes / 16));
+  a.num_rows = static_cast<int32_t>(p->num_rows);
+  a.page_size = static_cast<int32_t>(p->page_size);
+  a.table_width = static_cast<int32_t>(p->table_width);
+  const int64_t grid = (p->num_rows + kAppendRows - 1) / kAppendRows;
+  hipLaunchKernelGGL(fa2_kv_append_kernel, dim3(static_cast<uint32_t>(grid)),
+                     dim3(kAppendThreads), 0, static_cast<hipStream_t>(stream), a);
+  return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
+}
+

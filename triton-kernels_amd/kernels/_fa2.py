@@ -19,11 +19,12 @@ DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 MASK_NONE, MASK_TOP_LEFT, MASK_BOTTOM_RIGHT = 0, 1, 2
 MAX_SPLITS = 64
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every symbol include/fa2.h declares.
 EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_strerror", "fa2_decode_workspace_size",
-           "fa2_decode_fwd", "fa2_abi_version", "fa2_params_size")
+           "fa2_decode_fwd", "fa2_kv_append", "fa2_kv_append_params_size", "fa2_abi_version",
+           "fa2_params_size")
 
 
 class Fa2Params(ctypes.Structure):
@@ -62,6 +63,19 @@ class Fa2Params(ctypes.Structure):
     ]
 
 
+class KvAppendParams(ctypes.Structure):
+    """Mirror of ``struct fa2_kv_append_params`` (include/fa2.h)."""
+
+    _fields_ = [("dtype", ctypes.c_int32), ("reserved0", ctypes.c_int32)] + [
+        (n, ctypes.c_int64) for n in (
+            "batch", "kv_heads", "head_dim", "num_rows", "page_size", "num_pages",
+            "table_width", "k_table_stride", "v_table_stride", "new_ts", "new_hs",
+            "cache_ts", "cache_hs")] + [
+        (n, ctypes.c_void_p) for n in (
+            "k_new", "v_new", "k_cache", "v_cache", "new_indptr", "start_pos",
+            "k_block_table", "v_block_table")]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -88,14 +102,19 @@ def lib():
             L.fa2_decode_workspace_size.restype = ctypes.c_int
             L.fa2_decode_fwd.argtypes = [ctypes.POINTER(Fa2Params), ctypes.c_void_p]
             L.fa2_decode_fwd.restype = ctypes.c_int
+            L.fa2_kv_append.argtypes = [ctypes.POINTER(KvAppendParams), ctypes.c_void_p]
+            L.fa2_kv_append.restype = ctypes.c_int
+            L.fa2_kv_append_params_size.argtypes = []
+            L.fa2_kv_append_params_size.restype = ctypes.c_size_t
             L.fa2_strerror.argtypes = [ctypes.c_int]
             L.fa2_strerror.restype = ctypes.c_char_p
             L.fa2_abi_version.argtypes = []
             L.fa2_abi_version.restype = ctypes.c_int
             L.fa2_params_size.argtypes = []
             L.fa2_params_size.restype = ctypes.c_size_t
-            if L.fa2_params_size() != ctypes.sizeof(Fa2Params):
-                raise RuntimeError("libfa2.so: fa2_params layout mismatch with the binding")
+            if (L.fa2_params_size() != ctypes.sizeof(Fa2Params) or
+                    L.fa2_kv_append_params_size() != ctypes.sizeof(KvAppendParams)):
+                raise RuntimeError("libfa2.so: parameter struct layout mismatch with the binding")
             if L.fa2_abi_version() != ABI_VERSION:
                 raise RuntimeError(f"libfa2.so: ABI version {L.fa2_abi_version()}, binding "
                                    f"expects {ABI_VERSION}; rebuild the library")
@@ -124,5 +143,12 @@ def forward(p: Fa2Params, stream: int, decode: bool = False) -> None:
     """Enqueue ``fa2_fwd`` (or ``fa2_decode_fwd``) on the HIP stream ``stream``."""
     fn = lib().fa2_decode_fwd if decode else lib().fa2_fwd
     rc = fn(ctypes.byref(p), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise Fa2Error(rc)
+
+
+def kv_append(p: KvAppendParams, stream: int) -> None:
+    """Enqueue ``fa2_kv_append`` on the HIP stream ``stream``."""
+    rc = lib().fa2_kv_append(ctypes.byref(p), ctypes.c_void_p(stream))
     if rc != 0:
         raise Fa2Error(rc)

@@ -28,6 +28,9 @@ s1  paged speculative_decode_attention, causal, M 8 drafts, at the
     B16, QH8/KVH8, N 8192 + 8 drafts, D64, page 16, bf16
 s2  paged speculative_decode_attention, causal, M 8, serving shape of d2
     (context + 8 drafts per sequence), Hq32 Hkv8 D128 bf16
+a1  paged_kv_append: write c4's whole context (32 seqs, ctx ~ U[512,8192],
+    Hkv8 D128 bf16) into its shuffled K and V page pools (a prefill's cache
+    fill); HBM-bound copy, reported in GB/s of bytes read + written
 """
 
 from __future__ import annotations
@@ -37,7 +40,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-CONFIGS = ("c1", "c2", "c3", "c4", "c5", "d1", "d2", "s1", "s2")
+CONFIGS = ("c1", "c2", "c3", "c4", "c5", "d1", "d2", "s1", "s2", "a1")
 PAGE = 16
 
 
@@ -61,7 +64,10 @@ class Workload:
     q_heads: int = 0
     kv_heads: int = 0
     head_dim: int = 0
-    kind: str = "prefill"       # prefill (flash_attention_v2) | decode | speculative
+    kind: str = "prefill"       # prefill (flash_attention_v2) | decode | speculative | append
+    k_new: torch.Tensor | None = None     # append: rows to write [T, Hkv, D]
+    v_new: torch.Tensor | None = None
+    new_indptr: torch.Tensor | None = None
 
     def kwargs(self) -> dict:
         if self.kind == "decode":
@@ -80,7 +86,8 @@ class Workload:
 
     def to(self, device) -> "Workload":
         out = Workload(**{f: getattr(self, f) for f in self.__dataclass_fields__})
-        for n in ("q", "k", "v", "q_indptr", "kv_indptr", "k_block_table", "v_block_table"):
+        for n in ("q", "k", "v", "q_indptr", "kv_indptr", "k_block_table", "v_block_table",
+                  "k_new", "v_new", "new_indptr"):
             t = getattr(out, n)
             if t is not None:
                 setattr(out, n, t.to(device))
@@ -105,14 +112,19 @@ def visible_pairs(Lq: int, Lk: int, is_causal: bool, alignment: str = "top_left"
 
 def flops(w: Workload) -> float:
     """4 * D * Hq * sum of visible pairs (QK^T and PV, 2 FLOP per MAC)."""
+    if w.kind == "append":
+        return 0.0
     pairs = sum(visible_pairs(lq, lk, w.is_causal, w.causal_alignment)
                 for lq, lk in zip(w.q_lens, w.kv_lens))
     return 4.0 * w.head_dim * w.q_heads * pairs
 
 
 def hbm_bytes(w: Workload) -> float:
-    """Q and O once at Hq, K and V once at Hkv (tokens actually attended)."""
+    """Q and O once at Hq, K and V once at Hkv (tokens actually attended);
+    append: the new K and V rows read once and written once."""
     es = torch.tensor([], dtype=w.dtype).element_size()
+    if w.kind == "append":
+        return 2.0 * 2 * es * w.k_new.numel()
     if w.kind != "prefill":
         sq = sum(w.q_lens)
     else:
@@ -264,6 +276,18 @@ def make(name: str, dtype: torch.dtype | None = None, seed: int = 0,
                         q_heads=Hq, kv_heads=Hkv, head_dim=D)
     if name in ("d1", "d2", "s1", "s2"):
         return _make_decode(name, dtype or torch.bfloat16, gen)
+    if name == "a1":
+        c4 = make("c4", dtype=dtype, seed=seed)
+        T = sum(c4.kv_lens)
+        g2 = torch.Generator().manual_seed(seed + 1)
+        kn = _randn(g2, (T, c4.kv_heads, c4.head_dim), c4.dtype)
+        vn = _randn(g2, (T, c4.kv_heads, c4.head_dim), c4.dtype)
+        return Workload("a1", "paged", c4.dtype, c4.q, torch.zeros_like(c4.k),
+                        torch.zeros_like(c4.v), False, kv_indptr=c4.kv_indptr,
+                        k_block_table=c4.k_block_table, v_block_table=c4.v_block_table,
+                        kv_page_size=PAGE, q_lens=[0] * len(c4.kv_lens), kv_lens=c4.kv_lens,
+                        q_heads=c4.q_heads, kv_heads=c4.kv_heads, head_dim=c4.head_dim,
+                        kind="append", k_new=kn, v_new=vn, new_indptr=indptr(c4.kv_lens))
     raise KeyError(name)
 
 
