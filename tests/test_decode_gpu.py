@@ -135,6 +135,16 @@ def test_forced_splits(layout, splits):
     check(case, layout, run(case, layout, num_splits=splits))
 
 
+@pytest.mark.parametrize("B", [255, 256, 257, 700])
+@pytest.mark.parametrize("layout", ["ragged", "paged"])
+def test_batch_sizes_around_the_plan_fast_path(layout, B):
+    """The device plan ranks up to 256 sequences directly and counting-sorts
+    larger batches: either order must cover every sequence exactly once."""
+    case = make_decode_case(B, 4, 2, 64, 1, torch.bfloat16, layout, seed=3600 + B,
+                            kv_range=(1, 80))
+    check(case, layout, run(case, layout, decode=True))
+
+
 @pytest.mark.parametrize("layout", ["ragged", "paged"])
 def test_empty_and_single_key_sequences(layout):
     """A sequence without keys gives NaN (the reference's 0/0,

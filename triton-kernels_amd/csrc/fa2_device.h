@@ -58,6 +58,7 @@ constexpr int kWaveRows = 32;  // query rows per wave
 constexpr int kBN = 64;        // keys per KV tile
 constexpr int kCostBuckets = 4096;
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanFastBatch = 256;  // decode plans up to this batch rank items directly
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: P <= 2^8 between rescales
 // LDS operand reads are issued this many MFMAs ahead of their MFMA
 #ifndef FA2_READ_AHEAD
@@ -812,7 +813,8 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
 // ---------------------------------------------------------------------------
 // Plan kernel (ragged / paged): builds the (sequence, q-block) work list in
 // descending order of KV tiles to process (longest-processing-time first),
-// by a counting sort over tile counts.  One workgroup; no host sync.
+// by a counting sort over tile counts (small decode batches: by ranking each
+// sequence directly).  One workgroup; no host sync.
 // ---------------------------------------------------------------------------
 template <int MODE>
 __device__ __forceinline__ void seq_lens(const KArgs& a, int b, int& Lq, int& Lk) {
@@ -840,6 +842,28 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
   __shared__ int hist[kCostBuckets];
   __shared__ int scan[kPlanThreads];
   const int tid = threadIdx.x;
+  if (a.pack_m > 0 && a.q_len <= a.block_rows && a.batch <= kPlanFastBatch) {
+    // Decode with one q-block per sequence and a small batch: item b's
+    // position is its rank by cost (ties by sequence index), one pass.
+    int c = 0;
+    if (tid < a.batch) {
+      int Lq, Lk;
+      seq_lens<MODE>(a, tid, Lq, Lk);
+      c = block_cost(a.mask, 0, Lq, Lk, true);
+      scan[tid] = c;
+    }
+    __syncthreads();
+    if (tid < a.batch) {
+      int rank = 0;
+      for (int u = 0; u < a.batch; ++u) {
+        const int cu = scan[u];
+        rank += (cu > c || (cu == c && u < tid)) ? 1 : 0;
+      }
+      if (rank < a.work_ub) work[rank] = make_int2(tid, 0);
+    }
+    if (tid == 0) *work_count = a.batch < a.work_ub ? a.batch : a.work_ub;
+    return;
+  }
   for (int i = tid; i < kCostBuckets; i += kPlanThreads) hist[i] = 0;
   __syncthreads();
   for (int b = tid; b < a.batch; b += kPlanThreads) {
