@@ -13,10 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = [os.path.join(HERE, "csrc", "fa2_fwd.hip")]
-DEPS = SOURCES + [os.path.join(HERE, "csrc", h) for h in
-                  ("fa2_device.h", "fa2_kernel_lds.h", "fa2_kernel_pp.h")] + \
-    [os.path.join(ROOT, "include", "fa2.h")]
+SOURCES = [os.path.join(HERE, "csrc", "fa2_fwd.hip")]  # includes every csrc/*.h
 OUT = os.path.join(HERE, "kernels", "libfa2.so")
 
 FLAGS = [
