@@ -95,7 +95,7 @@ typedef struct fa2_params {
   int64_t batch;      /* B (ragged: q_indptr.numel()-1)                       */
   int64_t q_heads;    /* Hq                                                    */
   int64_t kv_heads;   /* Hkv, Hq % Hkv == 0; q head h reads kv head h*Hkv/Hq  */
-  int64_t head_dim;   /* D                                                     */
+  int64_t head_dim;   /* D: 16, 32, 64, 128 or 256                             */
   int64_t q_len;      /* dense/paged: M (rows per sequence); ragged: Tq       */
   int64_t kv_len;     /* dense: N; ragged: Tkv; paged: rows of the k/v caches
                          (pages*page_size), or 0 if unknown - per-sequence

@@ -106,6 +106,42 @@ def test_head_dim_128(layout, dtype, causal):
     check_all(case, layout, causal, outs)
 
 
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("D", [16, 32, 256])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("causal", CAUSAL_FLAGS)
+def test_other_head_dims(layout, D, dtype, causal):
+    """Head dims 16 and 32 (the register-staged kernel on 64-dim tiles, the
+    padding dims read as zeros and never stored) and 256 (its own
+    instantiation): the reference takes any power of two its tl.dot accepts."""
+    s = 1300 + D + int(causal) + 7 * DTYPES.index(dtype) + 17 * LAYOUTS.index(layout)
+    case = make_case(3, 8, 2, D, "self", dtype, layout, s)
+    outs, _ = run_case(case, layout, causal)
+    check_all(case, layout, causal, outs)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("D", [16, 32, 256])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_other_head_dims_mqa_cross(layout, D, splits):
+    case = make_case(3, 8, 1, D, "cross", torch.bfloat16, layout, 1400 + D + splits,
+                     kv_range=(100, 600), dense_kv_range=(300, 600))
+    outs, _ = run_case(case, layout, False, num_splits=splits)
+    check_all(case, layout, False, outs)
+
+
+@pytest.mark.parametrize("D", [16, 32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_small_head_dim_never_reads_past_its_row(D, dtype):
+    """Shuffled pool whose unused slots hold NaN, page size 1: the 64-dim
+    tiles' padding columns lie in the next rows of the pool, so reading them
+    (instead of zero-filling) would put NaN into the scores."""
+    case = make_case(4, 8, 2, D, "self", dtype, "paged", 1500 + D)
+    outs, _ = run_case(case, "paged", True, shuffled=True, seed=D, page=1)
+    assert not any(torch.isnan(o).any() for o in outs)
+    check_all(case, "paged", True, outs)
+
+
 EDGE_LENS = [1, 63, 64, 65, 127, 128, 129, 255, 257]
 
 

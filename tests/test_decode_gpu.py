@@ -117,6 +117,24 @@ def test_speculative_d128_many_rows(layout, heads, M, causal):
     check(case, layout, run(case, layout))
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("D", [16, 32, 256])
+def test_decode_other_head_dims(layout, D, dtype):
+    """Head dims 16, 32 and 256 run the register-staged kernel in packed mode."""
+    case = make_decode_case(4, 8, 2, D, 1, dtype, layout, seed=3500 + D)
+    check(case, layout, run(case, layout, decode=True))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("D", [32, 256])
+def test_speculative_other_head_dims(layout, D, causal):
+    case = make_decode_case(3, 8, 2, D, 4, torch.bfloat16, layout, seed=3600 + D, causal=causal,
+                            kv_range=(40, 400))
+    check(case, layout, run(case, layout))
+
+
 @pytest.mark.parametrize("page", [5, 8, 16, 32])
 @pytest.mark.parametrize("cache4d", [False, True])
 def test_paged_pools(page, cache4d):

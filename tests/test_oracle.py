@@ -93,6 +93,16 @@ def test_oracle_exact_vs_sdpa64(layout, attn_type, topology, causal):
 
 
 @pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("D", [16, 256])
+@pytest.mark.parametrize("causal", CAUSAL_FLAGS)
+def test_oracle_exact_vs_sdpa64_head_dims(layout, D, causal):
+    """The restatement at the smallest and largest head dims the kernels take."""
+    case = make_case(2, 4, 2, D, "self", torch.float32, layout, 40 + D + int(causal),
+                     q_range=(1, 70), kv_range=(1, 70), dense_q_range=(30, 70))
+    assert max_err(run_oracle(case, layout, causal), sdpa64(case, causal)) < 2e-5
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_oracle_reference_rounding_within_reference_tolerance(layout, dtype):
     case = make_case(3, 8, 2, 64, "self", dtype, layout, 11)

@@ -109,6 +109,11 @@ struct KArgs {
   // draft position: row r sees key j iff j <= Lk - pack_m + r % pack_m.
   int32_t pack_m;
   int32_t block_rows;   // unit rows per q-block of the launched kernel (kBM; decode kernel 64)
+  // Head dims the tensors hold (<= the kernel's D).  The register-staged
+  // kernel serves head_dim 16 and 32 with its D = 64 tiles: dims >= dv are
+  // read as zeros (they add nothing to Q.K^T and give zero output columns)
+  // and are never stored.
+  int32_t dv;
 };
 
 // ---------------------------------------------------------------------------
@@ -382,16 +387,21 @@ struct TileLoader {
   static constexpr int kRowsPerPass = kThreads / kTPR;
   static constexpr int kKPasses = kBN / kRowsPerPass;
   static constexpr int kKPT = kBN * D / (8 * kThreads);  // V keys per thread
-  static_assert(kKPasses >= 1 && kKPT >= 1 && kKPT <= 4, "tile shape");
+  static_assert(kKPasses >= 1 && (kKPT == 1 || kKPT == 2 || kKPT == 4 || kKPT == 8),
+                "tile shape");
+  // a 16-byte chunk outside the valid head dims: buffer offset past any range
+  static constexpr uint32_t kOut = 0xFFFFFF00u;
 
   Raw8<DT> kr[kKPasses];
   Raw8<DT> vr[kKPT];
   int krow0, vkey0, col;  // this thread's first K row, first V key, column (elements)
+  bool cok;               // col < dv: the column holds data (else zeros)
 
-  __device__ __forceinline__ TileLoader(int tid) {
+  __device__ __forceinline__ TileLoader(int tid, int dv) {
     krow0 = tid / kTPR;
     col = (tid % kTPR) * 8;
     vkey0 = (tid / kTPR) * kKPT;
+    cok = col < dv;
   }
 
   __device__ __forceinline__ static int paged_row(const int32_t* table, int64_t tstride, int b,
@@ -411,7 +421,7 @@ struct TileLoader {
           const int nc = min(n, w.Lk - 1);
           const uint32_t row = paged_row(a.k_table, a.k_table_stride, w.b, nc, a.page_size);
           const uint32_t off = row * static_cast<uint32_t>(a.k_ss * kEB) + col * kEB;
-          buf_raw8<DT>(kr[p], rs, n < w.Lk ? off : 0xFFFFFF00u);
+          buf_raw8<DT>(kr[p], rs, (n < w.Lk && cok) ? off : kOut);
         }
       } else {
         const uint32_t rsb = static_cast<uint32_t>(a.k_ss * kEB);
@@ -421,7 +431,7 @@ struct TileLoader {
             lim);
 #pragma unroll
         for (int p = 0; p < kKPasses; ++p)
-          buf_raw8<DT>(kr[p], rs, (krow0 + p * kRowsPerPass) * rsb + col * kEB);
+          buf_raw8<DT>(kr[p], rs, cok ? (krow0 + p * kRowsPerPass) * rsb + col * kEB : kOut);
       }
     } else {
 #pragma unroll
@@ -434,7 +444,10 @@ struct TileLoader {
                     a.k_ss;
         else
           off = w.k_base + static_cast<int64_t>(n) * a.k_ss;
-        load_raw8<DT>(kr[p], a.k, off + col);
+        if (cok)
+          load_raw8<DT>(kr[p], a.k, off + col);
+        else
+          zero_raw8<DT>(kr[p]);
       }
     }
   }
@@ -450,7 +463,7 @@ struct TileLoader {
           const int nc = min(n, w.Lk - 1);
           const uint32_t row = paged_row(a.v_table, a.v_table_stride, w.b, nc, a.page_size);
           const uint32_t off = row * static_cast<uint32_t>(a.v_ss * kEB) + col * kEB;
-          buf_raw8<DT>(vr[j], rs, n < w.Lk ? off : 0xFFFFFF00u);
+          buf_raw8<DT>(vr[j], rs, (n < w.Lk && cok) ? off : kOut);
         }
       } else {
         const uint32_t rsb = static_cast<uint32_t>(a.v_ss * kEB);
@@ -459,7 +472,8 @@ struct TileLoader {
             static_cast<const char*>(a.v) + (w.v_base + static_cast<int64_t>(k0) * a.v_ss) * kEB,
             lim);
 #pragma unroll
-        for (int j = 0; j < kKPT; ++j) buf_raw8<DT>(vr[j], rs, (vkey0 + j) * rsb + col * kEB);
+        for (int j = 0; j < kKPT; ++j)
+          buf_raw8<DT>(vr[j], rs, cok ? (vkey0 + j) * rsb + col * kEB : kOut);
       }
     } else {
 #pragma unroll
@@ -472,7 +486,10 @@ struct TileLoader {
                     a.v_ss;
         else
           off = w.v_base + static_cast<int64_t>(n) * a.v_ss;
-        load_raw8<DT>(vr[j], a.v, off + col);
+        if (cok)
+          load_raw8<DT>(vr[j], a.v, off + col);
+        else
+          zero_raw8<DT>(vr[j]);
       }
     }
   }
@@ -491,21 +508,26 @@ struct TileLoader {
     u32x4 x[kKPT];
 #pragma unroll
     for (int j = 0; j < kKPT; ++j) x[j] = to16<DT>(vr[j]);
-    const int pos = vpos(vkey0);  // kKPT <= 4 consecutive keys stay adjacent
+    // groups of up to 4 consecutive keys stay adjacent in a transposed row
+    constexpr int kG = kKPT < 4 ? kKPT : 4;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const int word = d >> 1;
-      // v_perm_b32 byte selectors: low halves (d even) or high halves (d odd)
-      const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
-      uint16_t* dst = vt + (col + d) * L::kVStride + pos;
-      if constexpr (kKPT == 4) {
-        const uint32_t a01 = __builtin_amdgcn_perm(x[1][word], x[0][word], sel);
-        const uint32_t a23 = __builtin_amdgcn_perm(x[3][word], x[2][word], sel);
-        *reinterpret_cast<u32x2*>(dst) = (u32x2){a01, a23};
-      } else if constexpr (kKPT == 2) {
-        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(x[1][word], x[0][word], sel);
-      } else {
-        *dst = static_cast<uint16_t>((d & 1) ? (x[0][word] >> 16) : (x[0][word] & 0xffffu));
+    for (int g0 = 0; g0 < kKPT; g0 += kG) {
+      const int pos = vpos(vkey0 + g0);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const int word = d >> 1;
+        // v_perm_b32 byte selectors: low halves (d even) or high halves (d odd)
+        const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+        uint16_t* dst = vt + (col + d) * L::kVStride + pos;
+        if constexpr (kG == 4) {
+          const uint32_t a01 = __builtin_amdgcn_perm(x[g0 + 1][word], x[g0][word], sel);
+          const uint32_t a23 = __builtin_amdgcn_perm(x[g0 + 3][word], x[g0 + 2][word], sel);
+          *reinterpret_cast<u32x2*>(dst) = (u32x2){a01, a23};
+        } else if constexpr (kG == 2) {
+          *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(x[1][word], x[0][word], sel);
+        } else {
+          *dst = static_cast<uint16_t>((d & 1) ? (x[0][word] >> 16) : (x[0][word] & 0xffffu));
+        }
       }
     }
   }
@@ -525,8 +547,9 @@ struct Pipe {
 #endif
 };
 
+// D = 256 holds one wave per SIMD (O^T alone is 128 VGPRs per lane).
 template <int DT, int D, int MODE, bool BUF, bool PIPE = Pipe<D>::value>
-__global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
+__global__ __launch_bounds__(kThreads, D > 128 ? 1 : 2) void fa2_fwd_kernel(KArgs a) {
   constexpr bool BF = Elt<DT>::kBF;
   constexpr int DC = D / 16;  // 16-wide head-dim chunks of Q^T (MFMA k-steps)
   constexpr int DB = D / 32;  // 32-row head-dim blocks of O^T
@@ -563,7 +586,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       Raw8<DT> r;
-      if (ok)
+      if (ok && c * 16 + hi * 8 < a.dv)
         load_raw8<DT>(r, a.q, base + c * 16);
       else
         zero_raw8<DT>(r);
@@ -585,7 +608,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
   const int qdiag = diag_row(a, qrow);
   const bool causal = a.mask != FA2_MASK_NONE;
 
-  TileLoader<DT, D, MODE, BUF> ld(tid);
+  TileLoader<DT, D, MODE, BUF> ld(tid, a.dv);
 
   // S^T block for the tile held in K buffer `kb`.
   auto compute_s = [&](f32x16 (&s)[SB], int kb) {
@@ -708,15 +731,21 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
       __syncthreads();
     }
     int i = 0;
-    for (; i + 2 < T; i += 2) {
-      step(NotLast{}, i, sA, sB);
-      step(NotLast{}, i + 1, sB, sA);
-    }
-    if (i + 1 < T) {
-      step(NotLast{}, i, sA, sB);
-      step(Last{}, i + 1, sB, sA);
-    } else {
+    if constexpr (D > 128) {
+      // one step per iteration: a second inlined step does not fit the registers
+      for (; i + 1 < T; ++i) step(NotLast{}, i, sA, sB);
       step(Last{}, i, sA, sB);
+    } else {
+      for (; i + 2 < T; i += 2) {
+        step(NotLast{}, i, sA, sB);
+        step(NotLast{}, i + 1, sB, sA);
+      }
+      if (i + 1 < T) {
+        step(NotLast{}, i, sA, sB);
+        step(Last{}, i + 1, sB, sA);
+      } else {
+        step(Last{}, i, sA, sB);
+      }
     }
   }
 
@@ -729,6 +758,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_kernel(KArgs a) {
       for (int d = 0; d < DB; ++d) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
+          if (d * 32 + g * 8 + hi * 4 >= a.dv) continue;  // padding dims (head_dim 16, 32)
           const int64_t off = base + d * 32 + g * 8;
           const float x0 = o[d][g * 4 + 0] * inv, x1 = o[d][g * 4 + 1] * inv;
           const float x2 = o[d][g * 4 + 2] * inv, x3 = o[d][g * 4 + 3] * inv;
@@ -778,6 +808,7 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   const int G = a.part_slots;
   const int R = a.part_rows;
   const int col = (threadIdx.x % kTPR) * 4;
+  if (col >= a.dv) return;  // padding dims (head_dim 16, 32 in D = 64 partials)
   for (int r = threadIdx.x / kTPR; r < R; r += kRowsPerPass) {
     const int qrow = q0 + r;
     if (qrow >= w.Lq) break;

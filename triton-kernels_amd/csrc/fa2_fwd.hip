@@ -57,6 +57,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 bool stride_ok(int64_t s, int eb) { return ((s * eb) & 15) == 0; }
 
+// Head dims the reference kernels take (a power of two that tl.dot accepts).
+bool head_dim_ok(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
+
+// The MFMA/LDS kernels are built for 64 and 128; the register-staged kernel
+// also for 256, and serves 16 and 32 with its D = 64 tiles (KArgs::dv).
+bool fast_dim(int64_t d) { return d == 64 || d == 128; }
+int64_t tile_dim(int64_t d) { return d < 64 ? 64 : d; }
+
 // Number of work units (q-block x head) the forward launch covers, and the
 // capacity of the ragged/paged work list.
 struct Plan {
@@ -67,6 +75,7 @@ struct Plan {
   int64_t grid_pp;  // its grid: npairs rounded up to kXcds, times Hq / Hkv / 2
   int splits;
   int part_rows;    // split partials: rows per slot
+  int64_t dim;      // head dims of the launched kernel's tiles (>= head_dim)
   int64_t rows;     // query rows of one unit's sequence (packed: Hq/Hkv * M)
   int block_rows;   // rows per q-block of the launched kernel
   bool dec;         // packed fp16/bf16: the decode kernel
@@ -96,7 +105,7 @@ int validate(const fa2_params* p) {
   if (p->layout < FA2_LAYOUT_DENSE || p->layout > FA2_LAYOUT_PAGED) return FA2_ERR_BAD_LAYOUT;
   if (p->dtype < FA2_DTYPE_F16 || p->dtype > FA2_DTYPE_F32) return FA2_ERR_BAD_DTYPE;
   if (p->mask < FA2_MASK_NONE || p->mask > FA2_MASK_CAUSAL_BOTTOM_RIGHT) return FA2_ERR_BAD_MASK;
-  if (p->head_dim != 64 && p->head_dim != 128) return FA2_ERR_HEAD_DIM;
+  if (!head_dim_ok(p->head_dim)) return FA2_ERR_HEAD_DIM;
   if (p->batch < 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->q_len < 0 || p->kv_len < 0)
     return FA2_ERR_BAD_SHAPE;
   if (p->q_heads % p->kv_heads != 0) return FA2_ERR_BAD_SHAPE;
@@ -162,7 +171,8 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   const int64_t group = p->q_heads / p->kv_heads;
   pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds * group;
   if (pl->grid_x > INT32_MAX || pl->npairs > INT32_MAX) return FA2_ERR_TOO_LARGE;
-  pl->pp = FA2_PP && p->dtype != FA2_DTYPE_F32 && group % 2 == 0;
+  pl->dim = tile_dim(p->head_dim);
+  pl->pp = FA2_PP && p->dtype != FA2_DTYPE_F32 && group % 2 == 0 && fast_dim(p->head_dim);
   pl->grid_pp = cdiv(pl->npairs, kXcds) * kXcds * cdiv(group, 2);
 
   int splits = p->num_splits;
@@ -211,7 +221,7 @@ int finish_plan(const fa2_params* p, Plan* pl) {
   off = (off + 255) & ~size_t(255);
   pl->off_o = off;
   if (splits > 1)
-    off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * p->head_dim * sizeof(float);
+    off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * pl->dim * sizeof(float);
   pl->total = off;
   return FA2_OK;
 }
@@ -225,9 +235,10 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   const int64_t group = p->q_heads / p->kv_heads;
   pl->rows = group * p->q_len;
   if (pl->rows > INT32_MAX / 2) return FA2_ERR_TOO_LARGE;
-  // fp16/bf16: the decode kernel (64-row blocks, one workgroup per CU);
-  // fp32: the register-staged kernel (128-row blocks, two per CU)
-  pl->dec = p->dtype != FA2_DTYPE_F32;
+  // fp16/bf16 at head_dim 64/128: the decode kernel (64-row blocks, one
+  // workgroup per CU); otherwise the register-staged kernel (128-row blocks)
+  pl->dim = tile_dim(p->head_dim);
+  pl->dec = p->dtype != FA2_DTYPE_F32 && fast_dim(p->head_dim);
   pl->block_rows = pl->dec ? kDecRows : kBM;
   const int64_t nqb = cdiv(pl->rows, pl->block_rows);
   pl->work_ub = nqb * p->batch;
@@ -266,7 +277,7 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
                        const_cast<int2*>(a.work), const_cast<int32_t*>(a.work_count));
   }
   const dim3 grid(pl.grid_x, pl.splits);
-  if constexpr (DT != FA2_DTYPE_F32) {
+  if constexpr (DT != FA2_DTYPE_F32 && (D == 64 || D == 128)) {
     if (pl.dec) {
       if (pl.buf)
         hipLaunchKernelGGL((fa2_decode_kernel<DT, D, MODE, true>), grid, dim3(kDecThreads), 0, st,
@@ -280,30 +291,39 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
       return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
     }
   }
-  if constexpr (DT == FA2_DTYPE_F32) {
+  bool generic = true;  // the register-staged kernel (fp32, other head dims)
+  if constexpr (DT != FA2_DTYPE_F32 && (D == 64 || D == 128)) {
+    if (a.dv == D) {
+      generic = false;
+      if (pl.pp) {
+        // persistent: one workgroup per CU walks the units (when not split)
+        int64_t wgs = pl.grid_pp;
+        if (pl.splits == 1 && FA2_PP_PERSISTENT) {
+          const int64_t cus = cu_count_current_device();
+          if (wgs > cus) wgs = cus;
+        }
+        const dim3 gpp(static_cast<uint32_t>(wgs), pl.splits);
+        if (pl.buf)
+          hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true>), gpp, dim3(kPPThreads), 0,
+                             st, a);
+        else
+          hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, false>), gpp, dim3(kPPThreads), 0,
+                             st, a);
+      } else {
+        if (pl.buf)
+          hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0,
+                             st, a);
+        else
+          hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0,
+                             st, a);
+      }
+    }
+  }
+  if (generic) {
     if (pl.buf)
       hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
     else
       hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st, a);
-  } else if (pl.pp) {
-    // persistent: one workgroup per CU walks the units (when not split)
-    int64_t wgs = pl.grid_pp;
-    if (pl.splits == 1 && FA2_PP_PERSISTENT) {
-      const int64_t cus = cu_count_current_device();
-      if (wgs > cus) wgs = cus;
-    }
-    const dim3 gpp(static_cast<uint32_t>(wgs), pl.splits);
-    if (pl.buf)
-      hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true>), gpp, dim3(kPPThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, false>), gpp, dim3(kPPThreads), 0, st,
-                         a);
-  } else {
-    if (pl.buf)
-      hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st,
-                         a);
   }
   if (pl.splits > 1) {
     hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), dim3(pl.grid_x), dim3(kThreads), 0, st,
@@ -321,10 +341,12 @@ int launch_mode(int mode, const KArgs& a, const Plan& pl, hipStream_t st) {
   }
 }
 
+// d: the plan's tile head dim (64 also serves head_dim 16 and 32)
 template <int DT>
-int launch_dim(int d, int mode, const KArgs& a, const Plan& pl, hipStream_t st) {
+int launch_dim(int64_t d, int mode, const KArgs& a, const Plan& pl, hipStream_t st) {
   if (d == 64) return launch_mode<DT, 64>(mode, a, pl, st);
-  return launch_mode<DT, 128>(mode, a, pl, st);
+  if (d == 128) return launch_mode<DT, 128>(mode, a, pl, st);
+  return launch_mode<DT, 256>(mode, a, pl, st);
 }
 
 }  // namespace
@@ -344,7 +366,7 @@ extern "C" const char* fa2_strerror(int s) {
     case FA2_ERR_BAD_DTYPE: return "dtype must be f16 (0), bf16 (1) or f32 (2)";
     case FA2_ERR_BAD_MASK: return "mask must be none (0), top-left causal (1) or bottom-right causal (2)";
     case FA2_ERR_BAD_SHAPE: return "invalid shape (negative size or q_heads % kv_heads != 0)";
-    case FA2_ERR_HEAD_DIM: return "unsupported head_dim (supported: 64, 128)";
+    case FA2_ERR_HEAD_DIM: return "unsupported head_dim (supported: 16, 32, 64, 128, 256)";
     case FA2_ERR_ALIGNMENT: return "tensor rows must start on 16-byte boundaries";
     case FA2_ERR_PAGED_ARGS: return "paged layout needs kv_indptr (lengths), both block tables and page_size > 0";
     case FA2_ERR_RAGGED_ARGS: return "ragged layout needs q_indptr and kv_indptr";
@@ -433,12 +455,13 @@ int run(const fa2_params* p, void* stream, bool packed) {
   a.part_o = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
   a.part_rows = pl.part_rows;
   a.pack_m = packed ? static_cast<int32_t>(p->q_len) : 0;
+  a.dv = static_cast<int32_t>(p->head_dim);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (p->dtype) {
-    case FA2_DTYPE_F16: return launch_dim<FA2_DTYPE_F16>(p->head_dim, p->layout, a, pl, st);
-    case FA2_DTYPE_BF16: return launch_dim<FA2_DTYPE_BF16>(p->head_dim, p->layout, a, pl, st);
-    default: return launch_dim<FA2_DTYPE_F32>(p->head_dim, p->layout, a, pl, st);
+    case FA2_DTYPE_F16: return launch_dim<FA2_DTYPE_F16>(pl.dim, p->layout, a, pl, st);
+    case FA2_DTYPE_BF16: return launch_dim<FA2_DTYPE_BF16>(pl.dim, p->layout, a, pl, st);
+    default: return launch_dim<FA2_DTYPE_F32>(pl.dim, p->layout, a, pl, st);
   }
 }
 

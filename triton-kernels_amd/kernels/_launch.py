@@ -17,7 +17,7 @@ DTYPES = {
     torch.bfloat16: _fa2.DTYPE_BF16,
     torch.float32: _fa2.DTYPE_F32,
 }
-SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
 def rows_ok(t: torch.Tensor) -> bool:
