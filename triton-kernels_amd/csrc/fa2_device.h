@@ -97,7 +97,7 @@ struct KArgs {
   float scale_log2;     // softmax_scale * log2(e)
   uint32_t pool_bytes_k;  // paged + buffer path: bytes of the k cache from the kv-head 0 row 0
   uint32_t pool_bytes_v;
-  const int2* work;     // ragged/paged work list (b, q-block), heaviest first
+  const int2* work;     // ragged/paged work list (b, q-block), heaviest first; null: no plan
   const int32_t* work_count;
   float* part_ml;       // split partials: (m, l) per row
   float* part_o;        // split partials: unnormalised O per row
@@ -296,11 +296,22 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1
     w.k_base = w.b * a.k_sb + w.kvh * a.k_sh;
     w.v_base = w.b * a.v_sb + w.kvh * a.v_sh;
   } else {
-    if (item >= *a.work_count) {
-      w.valid = false;
-      return w;
+    int2 it;
+    if (a.work) {
+      if (item >= *a.work_count) {
+        w.valid = false;
+        return w;
+      }
+      it = a.work[item];
+    } else {
+      // no plan (uniform q-block count, every workgroup resident at once, so
+      // the order does not matter): items in (q-block, sequence) order
+      if (item >= a.batch * a.nqb) {
+        w.valid = false;
+        return w;
+      }
+      it = make_int2(item % a.batch, item / a.batch);
     }
-    const int2 it = a.work[item];
     w.b = it.x;
     w.qblk = it.y;
     if constexpr (MODE == FA2_LAYOUT_RAGGED) {
