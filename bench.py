@@ -157,7 +157,33 @@ def main(argv=None):
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes")
+    ap.add_argument("--gemm-calibration", type=int, default=0, metavar="N",
+                    help="only time torch.matmul (hipBLASLt) bf16 N x N x N, --warmup + --steps "
+                         "back-to-back: the MFMA rate a library GEMM sustains on this GPU")
     args = ap.parse_args(argv)
+
+    if args.gemm_calibration:
+        n = args.gemm_calibration
+        g = torch.Generator(device="cuda:0").manual_seed(0)
+        a = torch.randn((n, n), device="cuda:0", generator=g).to(torch.bfloat16)
+        b = torch.randn((n, n), device="cuda:0", generator=g).to(torch.bfloat16)
+        c = torch.empty((n, n), device="cuda:0", dtype=torch.bfloat16)
+        for _ in range(args.warmup):
+            torch.matmul(a, b, out=c)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            torch.matmul(a, b, out=c)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        print(json.dumps({"gemm_calibration": f"bf16 {n}x{n}x{n} torch.matmul",
+                          "steps": args.steps, "warmup": args.warmup, "ms_per_gemm": round(ms, 5),
+                          "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_TFLOPS, 4)}),
+              flush=True)
+        return 0
 
     if args.copy_calibration:
         n = args.copy_calibration << 20
