@@ -238,7 +238,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
     for (int d = 0; d < DB; ++d) o[d] = (f32x16){};
     m_run = -INFINITY;
     l_run = 0.f;
-    if (!pre) load_q(u);
+    // group 1 loads its Q after the first barrier (below)
+    if (!pre && grp == 0) load_q(u);
 
     // M phase: PV of the previous tile, then S of this one.
     auto phase_m = [&](auto has_pv, auto has_s, int i) {
@@ -419,7 +420,14 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
         wait_vm((T > 1 ? 2 * kI : kI) + (pre ? kStores : 0));
       }
       pp_barrier();
-      if (grp != 0) pp_barrier();  // group 1 runs one phase behind
+      if (grp != 0) {
+        // Group 1 runs one phase behind.  Its Q loads go out now, under
+        // group 0's first MFMA phase, instead of competing for HBM with
+        // the loads that phase waits for (at a launch every workgroup
+        // fetches its first Q and tiles at once: ~4 us before any MFMA).
+        if (!pre) load_q(u);
+        pp_barrier();
+      }
       phase_m(N{}, Y{}, 0);
       pp_barrier();
       for (int i = 0; i + 1 < T; ++i) {
