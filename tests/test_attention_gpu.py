@@ -142,6 +142,23 @@ def test_small_head_dim_never_reads_past_its_row(D, dtype):
     check_all(case, "paged", True, outs)
 
 
+@pytest.mark.parametrize("L", [100, 300, 640, 1000])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mask", ["none", "top_left", "bottom_right"])
+def test_mha_dense_qblock_pairs(L, D, dtype, mask):
+    """MHA runs the two-head kernel with a pair of q-blocks of one head per
+    unit (odd q-block counts leave group 1 without rows in the last pair);
+    bottom-right uses a longer KV."""
+    causal = mask != "none"
+    align = "bottom_right" if mask == "bottom_right" else "top_left"
+    kvL = L + 77 if mask != "top_left" else L
+    case = make_case(2, 4, 4, D, "self" if kvL == L else "cross", dtype, "dense", 1600 + L + D,
+                     dense_q_range=(L, L), dense_kv_range=(kvL, kvL))
+    outs, _ = run_case(case, "dense", causal, alignment=align)
+    check_all(case, "dense", causal, outs, alignment=align)
+
+
 EDGE_LENS = [1, 63, 64, 65, 127, 128, 129, 255, 257]
 
 

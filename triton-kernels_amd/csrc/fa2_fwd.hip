@@ -72,6 +72,7 @@ struct Plan {
   int64_t npairs;   // work_ub * Hkv
   int64_t grid_x;   // npairs rounded up to kXcds, times Hq / Hkv
   bool pp;          // two-head ping-pong kernel
+  bool qpair;       // ... on MHA, two q-blocks of one head per unit (KArgs::qpair)
   int64_t grid_pp;  // its grid: npairs rounded up to kXcds, times Hq / Hkv / 2
   int splits;
   int part_rows;    // split partials: rows per slot
@@ -197,6 +198,17 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     }
   }
   pl->splits = splits;
+  // MHA, dense, one split: the two-head kernel pairs q-blocks of one head
+  // (+21 % over the one-head kernel on B2 H32 L2048 D128 causal bf16).
+  pl->qpair = FA2_PP && p->dtype != FA2_DTYPE_F32 && group == 1 &&
+              p->layout == FA2_LAYOUT_DENSE && fast_dim(p->head_dim) && splits == 1;
+  if (pl->qpair) {
+    pl->pp = true;
+    pl->work_ub = cdiv(nqb, 2) * p->batch;
+    pl->npairs = pl->work_ub * p->kv_heads;
+    pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds * group;
+    pl->grid_pp = cdiv(pl->npairs, kXcds) * kXcds;
+  }
   pl->rows = p->q_len;
   pl->block_rows = kBM;
   pl->dec = false;
@@ -248,6 +260,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds;
   if (pl->grid_x > INT32_MAX || pl->npairs > INT32_MAX) return FA2_ERR_TOO_LARGE;
   pl->pp = false;
+  pl->qpair = false;
   pl->grid_pp = 0;
   int splits = p->num_splits;
   if (splits == 0) {
@@ -448,6 +461,8 @@ int run(const fa2_params* p, void* stream, bool packed) {
   for (int s = 0; s < 31; ++s)
     if ((int64_t(1) << s) == a.page_size) a.page_shift = s;
   a.nqb = static_cast<int32_t>(cdiv(pl.rows, pl.block_rows));
+  a.qpair = pl.qpair ? 1 : 0;
+  if (pl.qpair) a.nqb = static_cast<int32_t>(cdiv(a.nqb, 2));  // q-block pairs
   a.block_rows = pl.block_rows;
   a.work_ub = static_cast<int32_t>(pl.work_ub);
   a.npairs = static_cast<int32_t>(pl.npairs);

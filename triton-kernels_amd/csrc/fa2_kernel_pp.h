@@ -151,11 +151,22 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   auto make_unit = [&](int L, PPUnit& u) -> bool {
     u.w = decode_work<MODE>(a, L, 2);
     if (!u.w.valid) return false;
-    u.hok = u.w.hg + grp < group;
-    u.q_base = u.w.q_base + grp * a.q_sh;
-    u.o_base = u.w.o_base + grp * a.o_sh;
-    u.q0 = u.w.qblk * kBM;
-    const int kv_end = kv_end_for_block(a.mask, u.q0, u.w.Lq, u.w.Lk, u.w.off);
+    int kv_end;
+    if (a.qpair) {  // MHA: q-blocks 2k (group 0) and 2k + 1 (group 1) of one head
+      const int qb = 2 * u.w.qblk;
+      u.q0 = (qb + grp) * kBM;
+      u.hok = u.q0 < u.w.Lq;
+      u.q_base = u.w.q_base;
+      u.o_base = u.w.o_base;
+      const int last = (qb + 1) * kBM < u.w.Lq ? qb + 1 : qb;  // same tiles for both groups
+      kv_end = kv_end_for_block(a.mask, last * kBM, u.w.Lq, u.w.Lk, u.w.off);
+    } else {
+      u.hok = u.w.hg + grp < group;
+      u.q_base = u.w.q_base + grp * a.q_sh;
+      u.o_base = u.w.o_base + grp * a.o_sh;
+      u.q0 = u.w.qblk * kBM;
+      kv_end = kv_end_for_block(a.mask, u.q0, u.w.Lq, u.w.Lk, u.w.off);
+    }
     const int ntiles = (kv_end + kBN - 1) / kBN;
     u.t_begin = (ntiles * split) / S;
     u.T = (ntiles * (split + 1)) / S - u.t_begin;
