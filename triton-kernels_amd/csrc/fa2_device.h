@@ -811,49 +811,70 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : 2) void fa2_fwd_kernel(KArg
 
 // ---------------------------------------------------------------------------
 // Split-KV combine: O = sum_s 2^(m_s-g) O_s / sum_s 2^(m_s-g) l_s, g = max m_s
-// (attention.py:710-724 restated in the log2 domain).
+// (attention.py:710-724 restated in the log2 domain).  Grid (units, row
+// chunks): each thread owns 4 columns of one row and walks the splits four
+// at a time, so the loads of different splits are in flight together (a
+// loop with one split per step is latency-bound at large split counts).
 // ---------------------------------------------------------------------------
+template <int D>
+constexpr int kCombineRows = kThreads / (D / 4);  // rows per workgroup
+
 template <int DT, int D, int MODE>
 __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   const Work w = decode_work<MODE>(a, blockIdx.x);
   if (!w.valid) return;
-  const int q0 = w.qblk * a.block_rows;
   constexpr int kTPR = D / 4;  // threads per row, 4 floats each
-  constexpr int kRowsPerPass = kThreads / kTPR;
-  const int S = a.num_splits;
-  const int G = a.part_slots;
-  const int R = a.part_rows;
+  const int r = blockIdx.y * kCombineRows<D> + threadIdx.x / kTPR;
   const int col = (threadIdx.x % kTPR) * 4;
-  if (col >= a.dv) return;  // padding dims (head_dim 16, 32 in D = 64 partials)
-  for (int r = threadIdx.x / kTPR; r < R; r += kRowsPerPass) {
-    const int qrow = q0 + r;
-    if (qrow >= w.Lq) break;
-    float g = -INFINITY;
-    for (int s = 0; s < S; ++s) {
-      const int64_t slot = static_cast<int64_t>(s) * G + blockIdx.x;
-      g = fmaxf(g, a.part_ml[(slot * R + r) * 2]);
+  const int qrow = w.qblk * a.block_rows + r;
+  if (r >= a.part_rows || qrow >= w.Lq || col >= a.dv) return;
+  const int S = a.num_splits;
+  const int64_t G = a.part_slots;
+  const int64_t R = a.part_rows;
+  const float* ml = a.part_ml + (static_cast<int64_t>(blockIdx.x) * R + r) * 2;
+  const float* po = a.part_o + (static_cast<int64_t>(blockIdx.x) * R + r) * D + col;
+  const int64_t ml_step = G * R * 2, o_step = G * R * D;  // one split further
+  float g = -INFINITY;
+  int s = 0;
+  for (; s + 4 <= S; s += 4) {
+    const float m0 = ml[(s + 0) * ml_step], m1 = ml[(s + 1) * ml_step];
+    const float m2 = ml[(s + 2) * ml_step], m3 = ml[(s + 3) * ml_step];
+    g = fmaxf(g, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
+  }
+  for (; s < S; ++s) g = fmaxf(g, ml[s * ml_step]);
+  const float g_use = (g == -INFINITY) ? 0.f : g;
+  float lsum = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  s = 0;
+  for (; s + 4 <= S; s += 4) {
+    float m[4], l[4];
+    f32x4 x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m[j] = ml[(s + j) * ml_step];
+      l[j] = ml[(s + j) * ml_step + 1];
+      x[j] = *reinterpret_cast<const f32x4*>(po + (s + j) * o_step);
     }
-    const float g_use = (g == -INFINITY) ? 0.f : g;
-    float lsum = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < S; ++s) {
-      const int64_t slot = static_cast<int64_t>(s) * G + blockIdx.x;
-      const float m = a.part_ml[(slot * R + r) * 2];
-      const float l = a.part_ml[(slot * R + r) * 2 + 1];
-      const float wgt = fast_exp2(m - g_use);
-      lsum += wgt * l;
-      const f32x4 x = *reinterpret_cast<const f32x4*>(a.part_o + (slot * R + r) * D + col);
-      acc += wgt * x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // splits in order, as the one-at-a-time loop
+      const float wgt = fast_exp2(m[j] - g_use);
+      lsum += wgt * l[j];
+      acc += wgt * x[j];
     }
-    const float inv = 1.f / lsum;
-    const int64_t off = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + col;
-    if constexpr (DT == FA2_DTYPE_F32) {
-      *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + off) = acc * inv;
-    } else {
-      constexpr bool BF = Elt<DT>::kBF;
-      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
-          (u32x2){pack2<BF>(acc[0] * inv, acc[1] * inv), pack2<BF>(acc[2] * inv, acc[3] * inv)};
-    }
+  }
+  for (; s < S; ++s) {
+    const float wgt = fast_exp2(ml[s * ml_step] - g_use);
+    lsum += wgt * ml[s * ml_step + 1];
+    acc += wgt * *reinterpret_cast<const f32x4*>(po + s * o_step);
+  }
+  const float inv = 1.f / lsum;  // 0/0 -> NaN for a row with no key, as the reference
+  const int64_t off = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + col;
+  if constexpr (DT == FA2_DTYPE_F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + off) = acc * inv;
+  } else {
+    constexpr bool BF = Elt<DT>::kBF;
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
+        (u32x2){pack2<BF>(acc[0] * inv, acc[1] * inv), pack2<BF>(acc[2] * inv, acc[3] * inv)};
   }
 }
 

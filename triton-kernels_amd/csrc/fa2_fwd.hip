@@ -180,7 +180,12 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   int splits = p->num_splits;
   if (splits == 0) {
     // Split the KV sweep only when the grid cannot fill the GPU (two
-    // resident workgroups per CU) and every split keeps >= 4 KV tiles.
+    // resident workgroups per CU) and every split keeps >= 16 KV tiles
+    // (1024 keys).  Measured on MI355X (bf16 D128): a split costs its fp32
+    // partials' round trip and the combine launch, so short KV runs best
+    // unsplit (B1 Hq32/8 L512 causal: 17.8 us unsplit, 21.9 at 2 splits;
+    // MHA L1024: 29.6 vs 39.1), while long KV with few units wants the
+    // splits (B1 Hq8 Lq128 Lk16384: 343 us unsplit, 34 at 16 splits).
     const int64_t cus = query_device ? cu_count_current_device() : 256;
     const int64_t slots = 2 * cus;
     int64_t kv_ub = p->kv_len;
@@ -190,7 +195,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     const int64_t units = pl->npairs * (p->q_heads / p->kv_heads);  // real workgroups
     if (units > 0 && units < slots) {
       int64_t s = cdiv(slots, units);
-      const int64_t by_tiles = tiles / 4;
+      const int64_t by_tiles = tiles / 16;
       if (s > by_tiles) s = by_tiles;
       if (s > FA2_MAX_SPLITS) s = FA2_MAX_SPLITS;
       if (s < 1) s = 1;
@@ -310,8 +315,9 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
         hipLaunchKernelGGL((fa2_decode_kernel<DT, D, MODE, false>), grid, dim3(kDecThreads), 0, st,
                            a);
       if (pl.splits > 1)
-        hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), dim3(pl.grid_x), dim3(kThreads), 0,
-                           st, a);
+        hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
+                           dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads),
+                           0, st, a);
       return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
     }
   }
@@ -350,7 +356,8 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
       hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st, a);
   }
   if (pl.splits > 1) {
-    hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), dim3(pl.grid_x), dim3(kThreads), 0, st,
+    hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
+                       dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads), 0, st,
                        a);
   }
   return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
