@@ -159,6 +159,26 @@ def test_mha_dense_qblock_pairs(L, D, dtype, mask):
     check_all(case, "dense", causal, outs, alignment=align)
 
 
+@pytest.mark.parametrize("layout", ["ragged", "paged"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("mask", ["none", "top_left", "bottom_right"])
+def test_mha_ragged_paged_qblock_pairs(layout, D, mask):
+    """Ragged / paged MHA whose sequences average >= 4 q-blocks run the
+    two-head kernel on q-block pairs (some sequences with an odd count)."""
+    causal = mask != "none"
+    align = "bottom_right" if mask == "bottom_right" else "top_left"
+    if layout == "ragged":
+        ql = [640, 1000, 300, 777]
+        kl = ql if mask == "top_left" else [n + 50 for n in ql]
+    else:
+        ql = [600] * 3
+        kl = [600, 1500, 700] if mask != "top_left" else [600] * 3
+    case = make_case(len(ql), 4, 4, D, "cross", torch.bfloat16, layout, 1650 + D,
+                     q_lens=ql, kv_lens=kl)
+    outs, _ = run_case(case, layout, causal, alignment=align, shuffled=layout == "paged", seed=D)
+    check_all(case, layout, causal, outs, alignment=align)
+
+
 EDGE_LENS = [1, 63, 64, 65, 127, 128, 129, 255, 257]
 
 

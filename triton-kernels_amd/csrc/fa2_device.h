@@ -114,7 +114,7 @@ struct KArgs {
   // read as zeros (they add nothing to Q.K^T and give zero output columns)
   // and are never stored.
   int32_t dv;
-  // Two-head kernel on MHA (Hq == Hkv, dense, one split): a unit is a pair
+  // Two-head kernel on MHA (Hq == Hkv, one split): a unit is a pair
   // of q-blocks (2k, 2k + 1) of one head, one per wave group, both over the
   // KV tiles of block 2k + 1 (the extra tiles are fully masked for block 2k
   // under a causal mask and add exact zeros); nqb then counts pairs.
@@ -904,6 +904,16 @@ __device__ __forceinline__ int block_cost(int mask, int j, int Lq, int Lk, bool 
   return tiles < kCostBuckets - 1 ? tiles : kCostBuckets - 1;
 }
 
+// Work items of a sequence with nq q-blocks: the q-blocks, or with
+// KArgs::qpair the pairs (2j, 2j + 1), which cost what block 2j + 1 (or a
+// lone last block 2j) costs.
+__device__ __forceinline__ int plan_items(const KArgs& a, int nq) {
+  return a.qpair ? (nq + 1) / 2 : nq;
+}
+__device__ __forceinline__ int plan_cost_block(const KArgs& a, int j, int nq) {
+  return a.qpair ? min(2 * j + 1, nq - 1) : j;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* work,
                                                                 int32_t* work_count) {
@@ -938,7 +948,8 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + a.block_rows - 1) / a.block_rows;
-    for (int j = 0; j < nq; ++j) atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk, a.pack_m > 0)], 1);
+    for (int j = 0; j < plan_items(a, nq); ++j)
+      atomicAdd(&hist[block_cost(a.mask, plan_cost_block(a, j, nq), Lq, Lk, a.pack_m > 0)], 1);
   }
   __syncthreads();
   // Exclusive scan in descending cost order: bucket c starts after all
@@ -972,8 +983,9 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + a.block_rows - 1) / a.block_rows;
-    for (int j = 0; j < nq; ++j) {
-      const int pos = atomicAdd(&hist[block_cost(a.mask, j, Lq, Lk, a.pack_m > 0)], 1);
+    for (int j = 0; j < plan_items(a, nq); ++j) {
+      const int pos =
+          atomicAdd(&hist[block_cost(a.mask, plan_cost_block(a, j, nq), Lq, Lk, a.pack_m > 0)], 1);
       if (pos < a.work_ub) work[pos] = make_int2(b, j);
     }
   }

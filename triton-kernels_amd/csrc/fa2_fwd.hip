@@ -203,13 +203,20 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     }
   }
   pl->splits = splits;
-  // MHA, dense, one split: the two-head kernel pairs q-blocks of one head
-  // (+21 % over the one-head kernel on B2 H32 L2048 D128 causal bf16).
-  pl->qpair = FA2_PP && p->dtype != FA2_DTYPE_F32 && group == 1 &&
-              p->layout == FA2_LAYOUT_DENSE && fast_dim(p->head_dim) && splits == 1;
+  // MHA, one split: the two-head kernel pairs q-blocks of one head (B2 H32
+  // L2048 D128 bf16: causal 660 -> 713 TFLOP/s, non-causal 803 -> 882).
+  // Ragged and paged only when sequences average >= 4 q-blocks: a sequence
+  // with one q-block leaves the second wave group without rows.
+  const bool many_qblocks = p->layout == FA2_LAYOUT_DENSE ||
+                            (p->layout == FA2_LAYOUT_PAGED && nqb >= 4) ||
+                            (p->layout == FA2_LAYOUT_RAGGED && p->batch > 0 &&
+                             p->q_len >= 4 * kBM * p->batch);
+  pl->qpair = FA2_PP && p->dtype != FA2_DTYPE_F32 && group == 1 && fast_dim(p->head_dim) &&
+              splits == 1 && many_qblocks;
   if (pl->qpair) {
     pl->pp = true;
-    pl->work_ub = cdiv(nqb, 2) * p->batch;
+    // ragged keeps its bound (sum over sequences of their pairs <= nqb + batch)
+    if (p->layout != FA2_LAYOUT_RAGGED) pl->work_ub = cdiv(nqb, 2) * p->batch;
     pl->npairs = pl->work_ub * p->kv_heads;
     pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds * group;
     pl->grid_pp = cdiv(pl->npairs, kXcds) * kXcds;
