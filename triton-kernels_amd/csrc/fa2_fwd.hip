@@ -328,25 +328,31 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
       return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
     }
   }
-  bool generic = true;  // the register-staged kernel (fp32, other head dims)
-  if constexpr (DT != FA2_DTYPE_F32 && (D == 64 || D == 128)) {
+  bool generic = true;  // the register-staged kernel (fp32, head dims 16 and 32)
+  if constexpr (DT != FA2_DTYPE_F32 && (D == 64 || D == 128 || D == 256)) {
     if (a.dv == D) {
       generic = false;
-      if (pl.pp) {
-        // persistent: one workgroup per CU walks the units (when not split)
-        int64_t wgs = pl.grid_pp;
-        if (pl.splits == 1 && FA2_PP_PERSISTENT) {
-          const int64_t cus = cu_count_current_device();
-          if (wgs > cus) wgs = cus;
+      // (the two-head kernel's three K/V slots do not fit LDS at D = 256)
+      bool launched = false;
+      if constexpr (D <= 128) {
+        if (pl.pp) {
+          // persistent: one workgroup per CU walks the units (when not split)
+          int64_t wgs = pl.grid_pp;
+          if (pl.splits == 1 && FA2_PP_PERSISTENT) {
+            const int64_t cus = cu_count_current_device();
+            if (wgs > cus) wgs = cus;
+          }
+          const dim3 gpp(static_cast<uint32_t>(wgs), pl.splits);
+          if (pl.buf)
+            hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true>), gpp, dim3(kPPThreads), 0,
+                               st, a);
+          else
+            hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, false>), gpp, dim3(kPPThreads), 0,
+                               st, a);
+          launched = true;
         }
-        const dim3 gpp(static_cast<uint32_t>(wgs), pl.splits);
-        if (pl.buf)
-          hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true>), gpp, dim3(kPPThreads), 0,
-                             st, a);
-        else
-          hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, false>), gpp, dim3(kPPThreads), 0,
-                             st, a);
-      } else {
+      }
+      if (!launched) {
         if (pl.buf)
           hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0,
                              st, a);

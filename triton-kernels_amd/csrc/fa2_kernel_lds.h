@@ -400,12 +400,12 @@ __device__ __forceinline__ void lds_fill_barrier() {
 #ifndef FA2_LDS_PIPE
 #define FA2_LDS_PIPE 1
 #endif
-#define FA2_LDS_PIPE_DEFAULT(D) (FA2_LDS_PIPE != 0)
+#define FA2_LDS_PIPE_DEFAULT(D) (FA2_LDS_PIPE != 0 && (D) <= 128)
 #ifndef FA2_SGB
 #define FA2_SGB 7
 #endif
 template <int DT, int D, int MODE, bool BUF, bool PIPE = FA2_LDS_PIPE_DEFAULT(D)>
-__global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kernel(KArgs a) {
+__global__ __launch_bounds__(kThreads, D > 128 ? 1 : FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kernel(KArgs a) {
   static_assert(DT != FA2_DTYPE_F32, "fp32 uses the register-staged kernel");
   constexpr bool BF = Elt<DT>::kBF;
   constexpr int DC = D / 16;  // MFMA k-steps of S (16 head dims each)
@@ -414,8 +414,10 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
   using G = SwzGeo<D>;
 
   __shared__ __attribute__((aligned(1024))) char lds[4 * G::kTileBytes];
-  char* kbuf[2] = {lds, lds + G::kTileBytes};
-  char* vbuf[2] = {lds + 2 * G::kTileBytes, lds + 3 * G::kTileBytes};
+  // K buffers 0, 1 then V buffers 0, 1 (addresses computed, not read from an
+  // array of LDS pointers, which a loop-carried index cannot select)
+  auto kbuf = [&](int j) { return lds + (j & 1) * G::kTileBytes; };
+  auto vbuf = [&](int j) { return lds + (2 + (j & 1)) * G::kTileBytes; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -509,12 +511,12 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
     const int k0 = t * kBN;
     if constexpr (!kLast) {
       if (PIPE ? (i + 2 < T) : true)
-        ld.template issue<false>(a, w, k0 + (PIPE ? 2 : 1) * kBN, kbuf[(PIPE ? i : i + 1) & 1]);
-      ld.template issue<true>(a, w, k0 + kBN, vbuf[(i + 1) & 1]);
+        ld.template issue<false>(a, w, k0 + (PIPE ? 2 : 1) * kBN, kbuf((PIPE ? i : i + 1) & 1));
+      ld.template issue<true>(a, w, k0 + kBN, vbuf((i + 1) & 1));
     }
     if (active) {
     // scores of tile i must exist before they are masked
-    if constexpr (!PIPE) compute_s(s_cur, kbuf[i & 1]);
+    if constexpr (!PIPE) compute_s(s_cur, kbuf(i & 1));
     if ((k0 + kBN > w.Lk) || (causal && (k0 + kBN - 1 > wq_diag + w.off))) {
       // key = k0 + 4*hi + c with c a compile-time offset per accumulator:
       // visible iff c <= lim (sequence end and, if causal, the diagonal)
@@ -529,7 +531,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
         }
       }
     }
-    if constexpr (!kLast && PIPE) compute_s(s_nxt, kbuf[(i + 1) & 1]);
+    if constexpr (!kLast && PIPE) compute_s(s_nxt, kbuf((i + 1) & 1));
 
     float mx = -INFINITY;
 #pragma unroll
@@ -591,7 +593,7 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
       for (int d = 0; d < DB; ++d) o[d] *= alpha;
     }
     // O^T += V^T P^T; V^T fragments from two transposed reads per MFMA
-    const lds_char_t* vl = to_lds(vbuf[i & 1]);
+    const lds_char_t* vl = to_lds(vbuf(i & 1));
 #pragma unroll
     for (int c = 0; c < kBN / 16; ++c) {
 #pragma unroll
@@ -627,26 +629,32 @@ __global__ __launch_bounds__(kThreads, FA2_LDS_OCCUPANCY) void fa2_fwd_lds_kerne
 
   f32x16 sA[SB], sB[SB];
   if (T > 0) {
-    ld.template issue<false>(a, w, t_begin * kBN, kbuf[0]);
-    ld.template issue<true>(a, w, t_begin * kBN, vbuf[0]);
-    if (PIPE && T > 1) ld.template issue<false>(a, w, (t_begin + 1) * kBN, kbuf[1]);
+    ld.template issue<false>(a, w, t_begin * kBN, kbuf(0));
+    ld.template issue<true>(a, w, t_begin * kBN, vbuf(0));
+    if (PIPE && T > 1) ld.template issue<false>(a, w, (t_begin + 1) * kBN, kbuf(1));
     lds_fill_barrier();
     if constexpr (PIPE) {
-      if (active) compute_s(sA, kbuf[0]);
-      // step 0 refills kbuf[0] with K(t0+2): every wave must have finished
+      if (active) compute_s(sA, kbuf(0));
+      // step 0 refills kbuf(0) with K(t0+2): every wave must have finished
       // reading K(t0) first (the barrier also waits for the LDS reads)
       __syncthreads();
     }
     int i = 0;
-    for (; i + 2 < T; i += 2) {
-      step(NotLast{}, i, sA, sB);
-      step(NotLast{}, i + 1, sB, sA);
-    }
-    if (i + 1 < T) {
-      step(NotLast{}, i, sA, sB);
-      step(Last{}, i + 1, sB, sA);
-    } else {
+    if constexpr (D > 128) {
+      // one step per iteration: a second inlined step does not fit the registers
+      for (; i + 1 < T; ++i) step(NotLast{}, i, sA, sB);
       step(Last{}, i, sA, sB);
+    } else {
+      for (; i + 2 < T; i += 2) {
+        step(NotLast{}, i, sA, sB);
+        step(NotLast{}, i + 1, sB, sA);
+      }
+      if (i + 1 < T) {
+        step(NotLast{}, i, sA, sB);
+        step(Last{}, i + 1, sB, sA);
+      } else {
+        step(Last{}, i, sA, sB);
+      }
     }
   }
 
