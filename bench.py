@@ -197,8 +197,9 @@ def main(argv=None):
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the flash_attention_v2 hot path has no "
-              "multi-GPU component in this build (see DESIGN.md for how it would shard)",
-              file=sys.stderr)
+              "multi-GPU component in this build (it would shard by (sequence, kv head) "
+              "with no communication, or over the keys with one log-sum-exp merge of "
+              "the per-row partials)", file=sys.stderr)
         return 2
 
     from kernels import _fa2, decode_attention, speculative_decode_attention
