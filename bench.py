@@ -7,17 +7,21 @@ resident in HBM.  Prints ONE JSON line (rank 0, N=1):
 
   value       algorithmic TFLOP/s of the whole step (host wall clock over K
               back-to-back steps, bracketed by torch.cuda.synchronize());
-  roofline    achieved TFLOP/s per launch from one pair of HIP events around
-              the K back-to-back steps on the stream the kernels run on,
-              against the dense bf16/fp16 MFMA peak (256 CU x 4096 FLOP/clk x
-              2.4 GHz); `traffic` = HBM bytes per launch from the committed
-              rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the same workload
-              (profiles/hbm_traffic.json), null if there is none;
+  roofline    achieved TFLOP/s per launch: the K back-to-back steps run in
+              --windows windows with one pair of HIP events each on the
+              stream the kernels run on; `achieved` uses the median of the
+              windows' mean step times; against the dense bf16/fp16 MFMA peak
+              (256 CU x 4096 FLOP/clk x 2.4 GHz); `traffic` = HBM bytes per
+              launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+              summary of the same workload (profiles/hbm_traffic.json), null
+              if there is none;
   cpu_baseline  the reference test suite's oracle (fp32 SDPA per sequence,
               oracle.sdpa_reference) on the host CPU, on a bounded sample.
 
   python bench.py [--steps K] [--warmup W] [--config c2] [--dtype bf16]
-                  [--no-cpu] [--flush]
+                  [--no-cpu] [--flush] [--windows 5]
+  python bench.py --sweep [--sweep-out FILE]   # the reference benchmark's
+                  shapes (benchmarks/attention.py), one table row per point
 
 ``--gpus N`` with N > 1 exits: this build measures one GPU.
 """
@@ -67,7 +71,8 @@ def cpu_baseline(w: W.Workload, budget_s: float = 20.0):
     units as fit the budget."""
     import oracle
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    affinity = len(os.sched_getaffinity(0))
+    cores = cpu_threads()
     torch.set_num_threads(cores)
     qs, ks, vs = W.sequences(w)
     g = w.q_heads // w.kv_heads
@@ -119,8 +124,86 @@ def cpu_baseline(w: W.Workload, budget_s: float = 20.0):
         "kind": "port",
         "sample": f"{len(sample)} of {len(units)} (sequence, kv-head group) units of "
                   f"{w.name}, fp32 SDPA per sequence with repeat_interleaved KV heads, "
-                  f"{amount} per rep, median of 3",
+                  f"{amount} per rep, median of 3; {cores} threads of the "
+                  f"{affinity} cores in this process's affinity mask",
     }
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: every core of the affinity mask, capped by
+    the host's CPU share for this job when the environment states one
+    (OMP_NUM_THREADS; the GPU boxes give one GPU's job 16 cores)."""
+    n = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return n
+
+
+def time_steps(step, steps: int, windows: int, stream):
+    """Run `steps` back-to-back steps in `windows` windows, one HIP event pair
+    per window on `stream`; returns (wall seconds, per-window mean ms)."""
+    windows = max(1, min(windows, steps))
+    sizes = [steps // windows + (1 if i < steps % windows else 0) for i in range(windows)]
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in sizes]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for (a, b), n in zip(ev, sizes):
+        a.record(stream)
+        for _ in range(n):
+            step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, [a.elapsed_time(b) / n for (a, b), n in zip(ev, sizes)]
+
+
+def median(xs):
+    xs = sorted(xs)
+    m = len(xs) // 2
+    return xs[m] if len(xs) % 2 else 0.5 * (xs[m - 1] + xs[m])
+
+
+def sweep(args) -> int:
+    """Time flash_attention_v2 (and v1) on every point of the reference
+    benchmark's sweep (workloads.sweep_points): one table row per point on
+    stdout, JSON lines to --sweep-out."""
+    from kernels.attention import flash_attention_v1, flash_attention_v2
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    out = open(args.sweep_out, "w") if args.sweep_out else None
+    print(f"{'layout':8}{'type':7}{'topo':6}{'mask':8}{'dtype':10}{'Q':>6}{'KV':>6}"
+          f"{'v2 us':>10}{'v2 TFLOP/s':>12}{'v1 us':>10}", flush=True)
+    for pt in W.sweep_points():
+        w = W.make_sweep(*pt).to(dev)
+        kw = w.kwargs()
+        res = {}
+        for name, fn in (("v2", flash_attention_v2), ("v1", flash_attention_v1)):
+            def step():
+                return fn(w.q, w.k, w.v, **kw)
+            for _ in range(args.warmup):
+                step()
+            _, win = time_steps(step, args.steps, args.windows, stream)
+            res[name] = median(win)
+        fl = W.flops(w)
+        layout, attn, topo, dt, causal, ql, kl = pt
+        tf = fl / (res["v2"] * 1e-3) / 1e12
+        print(f"{layout:8}{attn:7}{topo:6}{'causal' if causal else 'full':8}"
+              f"{DTYPE_NAME[dt]:10}{ql:>6}{w.kv_lens[0]:>6}{res['v2'] * 1e3:>10.1f}{tf:>12.1f}"
+              f"{res['v1'] * 1e3:>10.1f}", flush=True)
+        if out:
+            out.write(json.dumps({"layout": layout, "attn": attn, "topology": topo,
+                                  "dtype": DTYPE_NAME[dt], "causal": causal, "q_len": ql,
+                                  "kv_len": w.kv_lens[0], "batch": W.SWEEP_BATCH,
+                                  "head_dim": W.SWEEP_D, "gflop": round(fl / 1e9, 4),
+                                  "v2_ms": round(res["v2"], 5), "v1_ms": round(res["v1"], 5),
+                                  "v2_tflops": round(tf, 2)}) + "\n")
+        del w
+    if out:
+        out.close()
+    return 0
 
 
 def hbm_traffic(config: str, dtype: str):
@@ -154,6 +237,11 @@ def main(argv=None):
     ap.add_argument("--flush", action="store_true",
                     help="write 512 MiB between steps (outside the events) to flush L2/MALL")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--windows", type=int, default=5,
+                    help="event-pair windows over the timed steps (median of their means)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time the reference benchmark's sweep of shapes instead")
+    ap.add_argument("--sweep-out", default=None, help="JSON lines of the sweep")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes")
@@ -208,6 +296,8 @@ def main(argv=None):
     _fa2.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.sweep:
+        return sweep(args)
     dt = DTYPES[args.dtype] if args.dtype else None
     w_cpu = W.make(args.config, dtype=dt, causal_alignment=args.alignment)
     w = w_cpu.to(dev)
@@ -237,17 +327,10 @@ def main(argv=None):
 
     stream = torch.cuda.current_stream(dev)
     if flush_buf is None:
-        # back-to-back steps; one event pair on the kernels' stream
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record(stream)
-        for _ in range(args.steps):
-            step()
-        stop.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        kern_avg = start.elapsed_time(stop) / args.steps
+        # back-to-back steps; one event pair per window on the kernels' stream
+        wall, win = time_steps(step, args.steps, args.windows, stream)
+        kern_avg = median(win)
+        kern_mean = sum(win) / len(win)
         ms_per_step = wall * 1e3 / args.steps
     else:
         # cold caches: a flush between steps, each step between its own events
@@ -260,8 +343,11 @@ def main(argv=None):
             step()
             ev[i][1].record(stream)
         torch.cuda.synchronize()
-        kern_avg = sum(a.elapsed_time(b) for a, b in ev) / args.steps
-        ms_per_step = kern_avg  # wall clock would include the flush writes
+        per = [a.elapsed_time(b) for a, b in ev]
+        kern_avg = median(per)
+        kern_mean = sum(per) / len(per)
+        win = per
+        ms_per_step = kern_mean  # wall clock would include the flush writes
     bound = "mfma" if fl / nbytes > (PEAK_TFLOPS * 1e12) / (PEAK_HBM_GBS * 1e9) else "hbm"
     if bound == "mfma":
         metric, unit, peak, work = METRIC, "TFLOP/s", PEAK_TFLOPS, fl / 1e12
@@ -302,7 +388,12 @@ def main(argv=None):
             "unit": unit,
             "frac": round(achieved / peak, 4),
             "traffic": hbm_traffic(args.config, DTYPE_NAME[w.dtype]),
-            "kernel_ms_avg": round(kern_avg, 5),
+            "kernel_ms_median": round(kern_avg, 5),
+            "kernel_ms_mean": round(kern_mean, 5),
+            "timing": (f"median of {len(win)} event-pair windows over {args.steps} "
+                       "back-to-back steps" if flush_buf is None else
+                       f"median of {len(win)} per-step event pairs, caches flushed between "
+                       "steps") + "; shader clock not pinned (short runs boost higher)",
             "hbm_gbs_algorithmic": round(nbytes / (kern_avg * 1e-3) / 1e9, 1),
             "tflops_algorithmic": round(fl / (kern_avg * 1e-3) / 1e12, 2),
         },

@@ -122,10 +122,21 @@ typedef struct fa2_params {
   int64_t page_size;            /* tokens per page (paged only)              */
 
   float softmax_scale;          /* reference: head_dim ** -0.5 (:897)        */
-  int32_t reserved0;
+  /* Upper limit on the workgroups of the persistent forward kernel (fp16 /
+   * bf16 prefill with an even number of query heads per kv head, or MHA):
+   * 0 = one workgroup per compute unit.  A smaller value leaves compute
+   * units to concurrent work; each workgroup then walks more units.  No
+   * counterpart in the reference (its grid is fixed by :873-880). */
+  int32_t max_workgroups;
 
   void* workspace;              /* device scratch, >= fa2_fwd_workspace_size */
   size_t workspace_bytes;
+
+  /* An upper bound of every sequence's KV length, or 0 if unknown (paged:
+   * the wrapper passes block-table width * page_size, the reference's N,
+   * attention.py:834).  Used only to size the split-KV factor; lengths
+   * always come from kv_indptr. */
+  int64_t kv_len_max;
 } fa2_params;
 
 /* Bytes of device workspace fa2_fwd needs for `p` (0 is possible).

@@ -29,10 +29,12 @@ def reference_check(outs, refs32, dtype, N):
 
 
 def _stats(outs, refs):
+    """Max and RMS of |o - r| over the elements where r is not NaN (on r's device)."""
     mx, ss, n = 0.0, 0.0, 0
     for o, r in zip(outs, refs):
-        d = o.double().cpu() - r.double().cpu()
-        fin = ~torch.isnan(r.double().cpu())
+        r = r.double()
+        d = o.to(r.device).double() - r
+        fin = ~torch.isnan(r)
         d = d[fin]
         if d.numel() == 0:
             continue
@@ -46,8 +48,9 @@ def strict_check(outs, emul, truth64, dtype, scale_max=4.0, scale_rms=2.0):
     """outs: kernel outputs; emul: oracle outputs with the kernel's rounding (fp32);
     truth64: fp64 SDPA.  Also requires NaN exactly where the truth has NaN."""
     for o, t in zip(outs, truth64):
-        assert torch.equal(torch.isnan(o.float().cpu()), torch.isnan(t.cpu())), "NaN pattern differs"
-    emul_r = [e.to(dtype).float() for e in emul]
+        assert torch.equal(torch.isnan(o.to(t.device).float()), torch.isnan(t)), \
+            "NaN pattern differs"
+    emul_r = [e.to(dtype).float() for e in emul]  # (tensors may live on any one device)
     k_max, k_rms = _stats(outs, truth64)
     e_max, e_rms = _stats(emul_r, truth64)
     floor = ULP[dtype]
@@ -56,33 +59,51 @@ def strict_check(outs, emul, truth64, dtype, scale_max=4.0, scale_rms=2.0):
     return dict(kernel_max=k_max, kernel_rms=k_rms, emul_max=e_max, emul_rms=e_rms)
 
 
-def gpu_reference(q, k, v, is_causal, alignment="top_left", scale=None, row_chunk=2048):
-    """fp32 attention on the GPU for one sequence, q [Hq,Lq,D], k/v [Hkv,Lk,D].
+def gpu_attention(q, k, v, is_causal, alignment="top_left", scale=None, row_chunk=512,
+                  dtype=torch.float32, operand_round=None, p_round=None):
+    """Attention of one sequence on the GPU, q [Hq,Lq,D], k/v [Hkv,Lk,D].
 
-    Explicit fp32 matmuls with TF32 off (the SDPA math path, written out so
-    the reference never depends on a fused kernel); rows with no visible key
-    come out NaN like the reference's 0/0."""
+    ``dtype`` float32 with no rounding is the reference suite's oracle (fp32
+    SDPA math, tests/test_attention.py:80-98, written out as matmuls with
+    TF32 off so it never depends on a fused kernel); float64 is the truth
+    the strict bar measures errors against.  ``operand_round`` ("f16") and
+    ``p_round`` ("f16"/"bf16") emulate a kernel's rounding: operands rounded
+    before the products and the softmax weights exp(s - rowmax) rounded
+    before the P.V product and the row sum (computed in ``dtype``).  Rows
+    with no visible key come out NaN like the reference's 0/0.  Grouped heads
+    are computed per kv head (no repeated K/V)."""
     Hq, Lq, D = q.shape
     Hkv, Lk, _ = k.shape
     g = Hq // Hkv
     sc = D ** -0.5 if scale is None else scale
-    kf = k.float().repeat_interleave(g, 0)
-    vf = v.float().repeat_interleave(g, 0).contiguous()
-    kt = kf.transpose(1, 2).contiguous()
-    out = torch.empty((Hq, Lq, D), dtype=torch.float32, device=q.device)
+    rdt = {None: None, "none": None, "f16": torch.float16, "bf16": torch.bfloat16}
+
+    def prep(t):
+        r = rdt[operand_round]
+        t = t.to(r) if r is not None else t
+        return t.to(dtype)
+
+    out = torch.empty((Hq, Lq, D), dtype=dtype, device=q.device)
     prev = torch.backends.cuda.matmul.allow_tf32
     torch.backends.cuda.matmul.allow_tf32 = False
     try:
         off = (Lk - Lq) if alignment == "bottom_right" else 0
-        for r0 in range(0, Lq, row_chunk):
-            r1 = min(Lq, r0 + row_chunk)
-            s = torch.matmul(q[:, r0:r1].float().contiguous(), kt) * sc
-            if is_causal:
-                i = torch.arange(r0, r1, device=q.device)[:, None]
-                j = torch.arange(Lk, device=q.device)[None, :]
-                s = s.masked_fill(j > i + off, float("-inf"))
-            p = torch.softmax(s, dim=-1)
-            out[:, r0:r1] = torch.matmul(p, vf)
+        for h in range(Hkv):
+            kt = prep(k[h]).transpose(0, 1).contiguous()  # [D, Lk]
+            vh = prep(v[h]).contiguous()                   # [Lk, D]
+            qh = prep(q[h * g:(h + 1) * g])                # [g, Lq, D]
+            for r0 in range(0, Lq, row_chunk):
+                r1 = min(Lq, r0 + row_chunk)
+                s = torch.matmul(qh[:, r0:r1].contiguous(), kt) * sc
+                if is_causal:
+                    i = torch.arange(r0, r1, device=q.device)[:, None]
+                    j = torch.arange(Lk, device=q.device)[None, :]
+                    s = s.masked_fill(j > i + off, float("-inf"))
+                m = s.amax(dim=-1, keepdim=True)
+                p = torch.exp(s - m)
+                if rdt[p_round] is not None:
+                    p = p.to(rdt[p_round]).to(dtype)
+                out[h * g:(h + 1) * g, r0:r1] = torch.matmul(p, vh) / p.sum(-1, keepdim=True)
     finally:
         torch.backends.cuda.matmul.allow_tf32 = prev
     return out

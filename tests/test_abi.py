@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layout_matches():
     assert _fa2.lib().fa2_params_size() == ctypes.sizeof(_fa2.Fa2Params)
-    assert _fa2.lib().fa2_abi_version() == _fa2.ABI_VERSION == 3
+    assert _fa2.lib().fa2_abi_version() == _fa2.ABI_VERSION == 4
 
 
 def test_strerror_for_every_code():
@@ -70,6 +70,8 @@ def rc_fwd(p):
 @pytest.mark.parametrize("field,value,code", [
     ("layout", 3, 2), ("dtype", 7, 3), ("mask", 5, 4), ("q_heads", 7, 5), ("batch", -1, 5),
     ("head_dim", 96, 6), ("q_ss", 100, 7), ("num_splits", 65, 11), ("num_splits", -1, 11),
+    ("max_workgroups", -1, 5), ("kv_len_max", -1, 5),
+    ("k_ss", (1 << 24) + 8, 13),  # a 32 MiB+ row stride: tile offsets leave 32 bits
 ])
 def test_validation_errors(field, value, code):
     p = dense_params(**{field: value})
@@ -192,3 +194,32 @@ def test_decode_mqa_m1_any_head_stride():
     p = decode_params(1, kv_heads=8, q_sh=256, q_ss=128, o_sh=256, o_ss=128,
                       k_sb=8 * 300 * 128, v_sb=8 * 300 * 128)
     assert rc_dec(p)[0] == 0
+
+
+def paged_params(ctx_rows, **kw):
+    """Paged B1 Hq8 Hkv8 q128 D128 over a pool of ctx_rows rows, page 16."""
+    p = dense_params(layout=2, mask=0, num_splits=0, batch=1, q_heads=8, kv_heads=8, q_len=128,
+                     kv_len=ctx_rows, kv_indptr=16, k_block_table=16, v_block_table=16,
+                     page_size=16, k_table_stride=64, v_table_stride=64)
+    p.q_sb, p.q_sh, p.q_ss = 8 * 128 * 128, 128 * 128, 128
+    p.o_sb, p.o_sh, p.o_ss = p.q_sb, p.q_sh, p.q_ss
+    p.k_sb, p.k_sh, p.k_ss = 0, 128, 8 * 128
+    p.v_sb, p.v_sh, p.v_ss = 0, 128, 8 * 128
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_paged_split_bounded_by_pool_and_table():
+    """A short paged context is not split (no partials workspace): the split
+    count is bounded by the pool's rows, or by kv_len_max (table width x page
+    size), as dense and ragged calls are bounded by their KV length."""
+    rc, n = rc_ws(paged_params(208))
+    assert rc == 0 and n < 4096           # work list only
+    rc, n = rc_ws(paged_params(0, kv_len_max=208))
+    assert rc == 0 and n < 4096
+    rc, n = rc_ws(paged_params(1 << 20, kv_len_max=256))
+    assert rc == 0 and n < 4096
+    # an unknown bound keeps the old behaviour (split for parallelism)
+    rc, n = rc_ws(paged_params(0))
+    assert rc == 0 and n > (1 << 20)

@@ -392,10 +392,12 @@ __device__ __forceinline__ int vpos(int kk) {
 }
 
 // Global -> register staging of K and V tiles, then register -> LDS.
-// BUF: all byte offsets of the (sequence, kv-head) slice (dense/ragged) or of
-// the page pool (paged) fit in 31 bits; loads are buffer loads whose range
-// check zero-fills rows past the end.  !BUF: 64-bit global loads of rows
-// clamped to the last valid row (finite data, masked by the softmax).
+// Dense/ragged (BUF): buffer loads through one descriptor per tile, based at
+// the tile's first row (64-bit) and covering its rows inside the sequence,
+// whose range check zero-fills rows past the end.  Paged, BUF: the byte
+// offsets of every row of the page pool fit in 31 bits (buffer loads from
+// the pool base); !BUF: 64-bit global loads of rows clamped to the last
+// valid row (finite data, masked by the softmax).
 template <int DT, int D, int MODE, bool BUF>
 struct TileLoader {
   static constexpr int kEB = Elt<DT>::kBytes;
@@ -441,7 +443,8 @@ struct TileLoader {
         }
       } else {
         const uint32_t rsb = static_cast<uint32_t>(a.k_ss * kEB);
-        const uint32_t lim = static_cast<uint32_t>(w.Lk - k0) * rsb;
+        // the descriptor covers this tile's rows inside the sequence only
+        const uint32_t lim = static_cast<uint32_t>(min(max(w.Lk - k0, 0), kBN)) * rsb;
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(
             static_cast<const char*>(a.k) + (w.k_base + static_cast<int64_t>(k0) * a.k_ss) * kEB,
             lim);
@@ -483,7 +486,8 @@ struct TileLoader {
         }
       } else {
         const uint32_t rsb = static_cast<uint32_t>(a.v_ss * kEB);
-        const uint32_t lim = static_cast<uint32_t>(w.Lk - k0) * rsb;
+        // the descriptor covers this tile's rows inside the sequence only
+        const uint32_t lim = static_cast<uint32_t>(min(max(w.Lk - k0, 0), kBN)) * rsb;
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(
             static_cast<const char*>(a.v) + (w.v_base + static_cast<int64_t>(k0) * a.v_ss) * kEB,
             lim);

@@ -81,17 +81,23 @@ struct Plan {
   int block_rows;   // rows per q-block of the launched kernel
   bool dec;         // packed fp16/bf16: the decode kernel
   bool plan;        // ragged/paged: the plan kernel orders the work list
-  bool buf;         // K/V byte offsets fit the 31-bit buffer-load path
+  bool buf;         // paged: every row of the pool has a 31-bit byte offset
+  int64_t max_wgs;  // cap on the persistent grid (0: none)
   uint32_t pool_bytes_k, pool_bytes_v;
   size_t off_work, off_count, off_ml, off_o, total;
 };
 
-// Buffer loads address a K/V slice with 32-bit offsets and a range check.
-// Dense/ragged: the (sequence, kv head) slice is at most kv_len rows; paged:
-// the whole pool of kv_len rows.  Rows must not overlap (stride >= D).
+// K/V tiles are read through buffer descriptors.  Dense and ragged tiles, and
+// paged tiles whose page size is a multiple of the rows one DMA instruction
+// covers, get a descriptor per tile or page with a 64-bit base: any tensor
+// size.  The remaining paged loads (other page sizes, and the register-staged
+// kernel) address rows by 32-bit offsets from the pool base, which needs the
+// pool's size (kv_len rows) to fit 31 bits; otherwise they use 64-bit global
+// loads (the BUF = false kernels).  Rows must not overlap (stride >= D).
 bool buffer_path_ok(const fa2_params* p, uint32_t* kbytes, uint32_t* vbytes) {
   const int64_t eb = elt_bytes(p->dtype);
   const int64_t lim = (int64_t(1) << 31) - 1024;
+  if (p->layout != FA2_LAYOUT_PAGED) return true;
   if (p->kv_len <= 0) return false;
   if (p->k_ss < p->head_dim || p->v_ss < p->head_dim) return false;
   const int64_t kb = p->kv_len * p->k_ss * eb;
@@ -127,6 +133,12 @@ int validate(const fa2_params* p) {
   if (p->batch > lim || p->q_heads > 65536 || p->q_len > lim || p->kv_len > lim ||
       p->page_size > lim)
     return FA2_ERR_TOO_LARGE;
+  // a tile's (or page's) rows are addressed by 32-bit offsets from its first
+  // row: row strides up to 32 MiB
+  const int64_t row_lim = int64_t(1) << 25;
+  if (p->k_ss * eb > row_lim || p->v_ss * eb > row_lim || p->o_ss * eb > row_lim)
+    return FA2_ERR_TOO_LARGE;
+  if (p->max_workgroups < 0 || p->kv_len_max < 0) return FA2_ERR_BAD_SHAPE;
   return FA2_OK;
 }
 
@@ -159,6 +171,16 @@ bool empty_problem(const fa2_params* p) {
 
 int finish_plan(const fa2_params* p, Plan* pl);
 
+// Longest KV range any sequence can have, for the split heuristic (lengths
+// themselves live on the device): N (dense), Tkv (ragged), the pool's rows
+// (paged: a heuristic bound, pages may repeat), each capped by the caller's
+// kv_len_max (paged: block-table width * page_size).
+int64_t kv_upper_bound(const fa2_params* p) {
+  int64_t ub = p->kv_len > 0 ? p->kv_len : INT32_MAX;
+  if (p->kv_len_max > 0 && p->kv_len_max < ub) ub = p->kv_len_max;
+  return ub;
+}
+
 int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   const int64_t nqb = cdiv(p->q_len, kBM);
   if (p->layout == FA2_LAYOUT_DENSE)
@@ -188,9 +210,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     // splits (B1 Hq8 Lq128 Lk16384: 343 us unsplit, 34 at 16 splits).
     const int64_t cus = query_device ? cu_count_current_device() : 256;
     const int64_t slots = 2 * cus;
-    int64_t kv_ub = p->kv_len;
-    if (p->layout == FA2_LAYOUT_PAGED) kv_ub = INT32_MAX;  // lengths live on the device
-    const int64_t tiles = cdiv(kv_ub, kBN);
+    const int64_t tiles = cdiv(kv_upper_bound(p), kBN);
     splits = 1;
     const int64_t units = pl->npairs * (p->q_heads / p->kv_heads);  // real workgroups
     if (units > 0 && units < slots) {
@@ -234,6 +254,7 @@ int finish_plan(const fa2_params* p, Plan* pl) {
   const int splits = pl->splits;
   pl->pool_bytes_k = pl->pool_bytes_v = 0;
   pl->buf = buffer_path_ok(p, &pl->pool_bytes_k, &pl->pool_bytes_v);
+  pl->max_wgs = p->max_workgroups;
 
   size_t off = 0;
   pl->off_work = off;
@@ -280,8 +301,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
     // the decode kernel holds a CU alone: one workgroup per CU (measured on
     // MI355X: 128 units of 128 tiles run best at 2 splits, 512 units at 1)
     const int64_t target = cus;
-    // longest possible sequence: N (dense), Tkv (ragged), the pool (paged)
-    const int64_t tiles = cdiv(p->kv_len > 0 ? p->kv_len : INT32_MAX, kBN);
+    const int64_t tiles = cdiv(kv_upper_bound(p), kBN);
     splits = 1;
     if (pl->npairs > 0 && pl->npairs < target) {
       int64_t sp = cdiv(target, pl->npairs);
@@ -305,6 +325,19 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   return finish_plan(p, pl);
 }
 
+// Launch kernel K<..., BUF> with BUF = pl.buf; only paged layouts ever run
+// the BUF = false kernels (dense and ragged tiles are always rebased).
+#define FA2_LAUNCH_BUF(KERNEL, GRID, BLOCK)                                       \
+  do {                                                                           \
+    if constexpr (MODE == FA2_LAYOUT_PAGED) {                                    \
+      if (!pl.buf) {                                                             \
+        hipLaunchKernelGGL((KERNEL<DT, D, MODE, false>), GRID, BLOCK, 0, st, a); \
+        break;                                                                   \
+      }                                                                          \
+    }                                                                            \
+    hipLaunchKernelGGL((KERNEL<DT, D, MODE, true>), GRID, BLOCK, 0, st, a);      \
+  } while (0)
+
 template <int DT, int D, int MODE>
 int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
   if constexpr (MODE != FA2_LAYOUT_DENSE) {
@@ -315,12 +348,7 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
   const dim3 grid(pl.grid_x, pl.splits);
   if constexpr (DT != FA2_DTYPE_F32 && (D == 64 || D == 128)) {
     if (pl.dec) {
-      if (pl.buf)
-        hipLaunchKernelGGL((fa2_decode_kernel<DT, D, MODE, true>), grid, dim3(kDecThreads), 0, st,
-                           a);
-      else
-        hipLaunchKernelGGL((fa2_decode_kernel<DT, D, MODE, false>), grid, dim3(kDecThreads), 0, st,
-                           a);
+      FA2_LAUNCH_BUF(fa2_decode_kernel, grid, dim3(kDecThreads));
       if (pl.splits > 1)
         hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
                            dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads),
@@ -336,38 +364,22 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
       bool launched = false;
       if constexpr (D <= 128) {
         if (pl.pp) {
-          // persistent: one workgroup per CU walks the units (when not split)
+          // persistent: at most one workgroup per CU walks the units
           int64_t wgs = pl.grid_pp;
           if (pl.splits == 1 && FA2_PP_PERSISTENT) {
             const int64_t cus = cu_count_current_device();
             if (wgs > cus) wgs = cus;
           }
+          if (pl.max_wgs > 0 && wgs > pl.max_wgs) wgs = pl.max_wgs;
           const dim3 gpp(static_cast<uint32_t>(wgs), pl.splits);
-          if (pl.buf)
-            hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true>), gpp, dim3(kPPThreads), 0,
-                               st, a);
-          else
-            hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, false>), gpp, dim3(kPPThreads), 0,
-                               st, a);
+          FA2_LAUNCH_BUF(fa2_fwd_pp_kernel, gpp, dim3(kPPThreads));
           launched = true;
         }
       }
-      if (!launched) {
-        if (pl.buf)
-          hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0,
-                             st, a);
-        else
-          hipLaunchKernelGGL((fa2_fwd_lds_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0,
-                             st, a);
-      }
+      if (!launched) FA2_LAUNCH_BUF(fa2_fwd_lds_kernel, grid, dim3(kThreads));
     }
   }
-  if (generic) {
-    if (pl.buf)
-      hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, true>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((fa2_fwd_kernel<DT, D, MODE, false>), grid, dim3(kThreads), 0, st, a);
-  }
+  if (generic) FA2_LAUNCH_BUF(fa2_fwd_kernel, grid, dim3(kThreads));
   if (pl.splits > 1) {
     hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
                        dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads), 0, st,
@@ -398,7 +410,7 @@ int launch_dim(int64_t d, int mode, const KArgs& a, const Plan& pl, hipStream_t 
 
 using namespace fa2;
 
-extern "C" int fa2_abi_version(void) { return 3; }
+extern "C" int fa2_abi_version(void) { return 4; }
 
 extern "C" size_t fa2_params_size(void) { return sizeof(fa2_params); }
 

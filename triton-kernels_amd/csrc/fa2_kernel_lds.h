@@ -174,7 +174,19 @@ struct DirectLoader {
   // Callers that read the table ahead of its use (decode producers): true
   // when one table entry serves each wave's kSpan rows of a tile.
   __device__ __forceinline__ static bool uniform_pages(const KArgs& a) {
-    return MODE == FA2_LAYOUT_PAGED && BUF && a.page_size % kSpan == 0;
+    return MODE == FA2_LAYOUT_PAGED && a.page_size % kSpan == 0;
+  }
+
+  // Descriptor of `rows` cache rows starting at physical row `prow` of the
+  // pool at `pool` (64-bit base on the scalar unit, so the pool may exceed
+  // the 32-bit offset range).  A row outside the pool (when its size is
+  // known: kv_len > 0) gets an empty range: the loads return zeros instead
+  // of reading outside the allocation.
+  __device__ __forceinline__ static u32x4 page_rsrc(const KArgs& a, const char* pool, int prow,
+                                                    int rows, uint32_t rsb) {
+    const bool inside = prow >= 0 && (a.kv_len <= 0 || prow <= a.kv_len - rows);
+    const char* base = pool + (inside ? static_cast<int64_t>(prow) * rsb : 0);
+    return rsrc_words(base, inside ? static_cast<uint32_t>(rows) * rsb : 0u);
   }
 
   // Block-table entry of this wave's first row of the tile at k0, through a
@@ -200,16 +212,15 @@ struct DirectLoader {
     const int64_t base = IS_V ? w.v_base : w.k_base;
     const uint32_t ldst = lds_addr_of(dst) + wave * kInstr * 1024;
     const uint32_t rsb = static_cast<uint32_t>((IS_V ? a.v_ss : a.k_ss) * kEB);
-    const u32x4 rsrc = rsrc_words(static_cast<const char*>(src) + base * kEB,
-                                  IS_V ? a.pool_bytes_v : a.pool_bytes_k);
     const int n0 = k0 + wave * kSpan;
     const int nc = min(n0, w.Lk - 1);
     const int poff = a.page_shift >= 0 ? (nc & (a.page_size - 1)) : nc % a.page_size;
-    const uint32_t urow =
-        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(page * a.page_size + poff));
+    const int prow = __builtin_amdgcn_readfirstlane(page * a.page_size + poff);
+    const u32x4 rsrc =
+        page_rsrc(a, static_cast<const char*>(src) + base * kEB, prow, kSpan, rsb);
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
-      const uint32_t off = (urow + j * kRPI) * rsb + (IS_V ? vvo[j] : kvo[j]);
+      const uint32_t off = j * kRPI * rsb + (IS_V ? vvo[j] : kvo[j]);
       dma_buffer_x4(rsrc, ldst + j * 1024, n0 + j * kRPI + lane_row() < w.Lk ? off : 0xFFFFFF00u);
     }
   }
@@ -221,78 +232,75 @@ struct DirectLoader {
   }
 
   // Issue the loads of one tile of K (IS_V=false) or V into `dst`.
+  // Dense/ragged: one descriptor per tile, based at the tile's first row and
+  // covering only its rows inside the sequence (rows past the end read as
+  // zeros).  Paged with page_size a multiple of the rows one wave (kSpan) or
+  // one instruction (kRPI) covers: one scalar table read and one descriptor
+  // per wave or per instruction, based at that physical row.  Every
+  // descriptor has a 64-bit base and a small range, so the size of the
+  // tensor or pool is not limited by the 32-bit buffer offsets.  Other page
+  // sizes look up every lane's row: through 32-bit offsets from the pool
+  // base when the pool fits them (BUF), else through 64-bit addresses.
   template <bool IS_V>
   __device__ __forceinline__ void issue(const KArgs& a, const Work& w, int k0, void* dst) const {
     const void* src = IS_V ? a.v : a.k;
     const int64_t rs = IS_V ? a.v_ss : a.k_ss;
     const int64_t base = IS_V ? w.v_base : w.k_base;
     const uint32_t ldst = lds_addr_of(dst) + wave * kInstr * 1024;
-    if constexpr (BUF) {
-      const uint32_t rsb = static_cast<uint32_t>(rs * kEB);
-      if constexpr (MODE == FA2_LAYOUT_PAGED) {
-        const u32x4 rsrc = rsrc_words(static_cast<const char*>(src) + base * kEB,
-                                      IS_V ? a.pool_bytes_v : a.pool_bytes_k);
-        const int32_t* tbl = IS_V ? a.v_table : a.k_table;
-        const int64_t ts = IS_V ? a.v_table_stride : a.k_table_stride;
-        if (a.page_size % kSpan == 0) {
-          // the wave's kSpan rows (starting at a multiple of kSpan) lie in
-          // one page: one table read for all its instructions
-          const int n0 = k0 + wave * kSpan;  // uniform
-          const uint32_t urow =
-              static_cast<uint32_t>(paged_row_uniform(a, tbl, ts, w.b, min(n0, w.Lk - 1)));
+    const uint32_t rsb = static_cast<uint32_t>(rs * kEB);
+    if constexpr (MODE == FA2_LAYOUT_PAGED) {
+      const char* pool = static_cast<const char*>(src) + base * kEB;
+      const int32_t* tbl = IS_V ? a.v_table : a.k_table;
+      const int64_t ts = IS_V ? a.v_table_stride : a.k_table_stride;
+      if (a.page_size % kSpan == 0) {
+        // the wave's kSpan rows (starting at a multiple of kSpan) lie in
+        // one page: one table read for all its instructions
+        const int n0 = k0 + wave * kSpan;  // uniform
+        const int prow = paged_row_uniform(a, tbl, ts, w.b, min(n0, w.Lk - 1));
+        const u32x4 rsrc = page_rsrc(a, pool, prow, kSpan, rsb);
 #pragma unroll
-          for (int j = 0; j < kInstr; ++j) {
-            const uint32_t off = (urow + j * kRPI) * rsb + (IS_V ? vvo[j] : kvo[j]);
-            dma_buffer_x4(rsrc, ldst + j * 1024,
-                          n0 + j * kRPI + lane_row() < w.Lk ? off : 0xFFFFFF00u);
-          }
-        } else if (a.page_size % kRPI == 0) {
+        for (int j = 0; j < kInstr; ++j) {
+          const uint32_t off = j * kRPI * rsb + (IS_V ? vvo[j] : kvo[j]);
+          dma_buffer_x4(rsrc, ldst + j * 1024,
+                        n0 + j * kRPI + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+        }
+      } else if (a.page_size % kRPI == 0) {
 #pragma unroll
-          for (int j = 0; j < kInstr; ++j) {
-            const int n0 = k0 + (wave * kInstr + j) * kRPI;  // uniform
-            const int n0c = min(n0, w.Lk - 1);
-            const uint32_t urow =
-                static_cast<uint32_t>(paged_row_uniform(a, tbl, ts, w.b, n0c));
-            const uint32_t off = urow * rsb + (IS_V ? vvo[j] : kvo[j]);
-            dma_buffer_x4(rsrc, ldst + j * 1024,
-                          n0 + lane_row() < w.Lk ? off : 0xFFFFFF00u);
-          }
-        } else {
+        for (int j = 0; j < kInstr; ++j) {
+          const int n0 = k0 + (wave * kInstr + j) * kRPI;  // uniform
+          const int prow = paged_row_uniform(a, tbl, ts, w.b, min(n0, w.Lk - 1));
+          const u32x4 rsrc = page_rsrc(a, pool, prow, kRPI, rsb);
+          const uint32_t off = IS_V ? vvo[j] : kvo[j];
+          dma_buffer_x4(rsrc, ldst + j * 1024, n0 + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+        }
+      } else if constexpr (BUF) {
+        const u32x4 rsrc = rsrc_words(pool, IS_V ? a.pool_bytes_v : a.pool_bytes_k);
 #pragma unroll
-          for (int j = 0; j < kInstr; ++j) {
-            const int r = row_of(j);
-            const int n = k0 + r;
-            const int nc = min(n, w.Lk - 1);
-            const uint32_t prow =
-                static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
-            const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
-            dma_buffer_x4(rsrc, ldst + j * 1024, n < w.Lk ? prow * rsb + col : 0xFFFFFF00u);
-          }
+        for (int j = 0; j < kInstr; ++j) {
+          const int r = row_of(j);
+          const int n = k0 + r;
+          const int nc = min(n, w.Lk - 1);
+          const uint32_t prow = static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
+          const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
+          dma_buffer_x4(rsrc, ldst + j * 1024, n < w.Lk ? prow * rsb + col : 0xFFFFFF00u);
         }
       } else {
-        // rows past the sequence read as zeros (a tile wholly past it: none)
-        const uint32_t lim = static_cast<uint32_t>(max(w.Lk - k0, 0)) * rsb;
-        const u32x4 rsrc = rsrc_words(
-            static_cast<const char*>(src) + (base + static_cast<int64_t>(k0) * rs) * kEB, lim);
 #pragma unroll
-        for (int j = 0; j < kInstr; ++j)
-          dma_buffer_x4(rsrc, ldst + j * 1024, IS_V ? vvo[j] : kvo[j]);
+        for (int j = 0; j < kInstr; ++j) {
+          const int r = row_of(j);
+          const int n = min(k0 + r, w.Lk - 1);  // clamped: finite data, masked later
+          const int64_t prow = paged_row(tbl, ts, w.b, n, a.page_size);
+          const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
+          dma_global_x4(pool + prow * rs * kEB + col, ldst + j * 1024);
+        }
       }
     } else {
+      // rows past the sequence read as zeros (a tile wholly past it: none)
+      const uint32_t lim = static_cast<uint32_t>(min(max(w.Lk - k0, 0), kBN)) * rsb;
+      const u32x4 rsrc = rsrc_words(
+          static_cast<const char*>(src) + (base + static_cast<int64_t>(k0) * rs) * kEB, lim);
 #pragma unroll
-      for (int j = 0; j < kInstr; ++j) {
-        const int r = row_of(j);
-        const int n = min(k0 + r, w.Lk - 1);  // clamped: finite data, masked later
-        int64_t r64;
-        if constexpr (MODE == FA2_LAYOUT_PAGED)
-          r64 = paged_row(IS_V ? a.v_table : a.k_table, IS_V ? a.v_table_stride : a.k_table_stride,
-                          w.b, n, a.page_size);
-        else
-          r64 = n;
-        const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
-        dma_global_x4(static_cast<const char*>(src) + (base + r64 * rs) * kEB + col,
-                      ldst + j * 1024);
-      }
+      for (int j = 0; j < kInstr; ++j) dma_buffer_x4(rsrc, ldst + j * 1024, IS_V ? vvo[j] : kvo[j]);
     }
   }
 };

@@ -19,7 +19,7 @@ DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 MASK_NONE, MASK_TOP_LEFT, MASK_BOTTOM_RIGHT = 0, 1, 2
 MAX_SPLITS = 64
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Every symbol include/fa2.h declares.
 EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_strerror", "fa2_decode_workspace_size",
@@ -57,9 +57,10 @@ class Fa2Params(ctypes.Structure):
         ("v_table_stride", ctypes.c_int64),
         ("page_size", ctypes.c_int64),
         ("softmax_scale", ctypes.c_float),
-        ("reserved0", ctypes.c_int32),
+        ("max_workgroups", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("kv_len_max", ctypes.c_int64),
     ]
 
 

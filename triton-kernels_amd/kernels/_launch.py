@@ -73,19 +73,23 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
             q_heads: int, kv_heads: int, head_dim: int, q_len: int, kv_len: int,
             q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
             q_strides, o_strides, qi=None, kvi=None, kt=None, vt=None,
-            page_size=None) -> None:
+            page_size=None, max_workgroups: int = 0, kv_len_max: int = 0) -> None:
     """Fill ``fa2_params`` and enqueue ``fa2_fwd`` (``decode=False``) or
     ``fa2_decode_fwd`` on torch's current stream of ``q``'s device.
 
     ``q_strides`` / ``o_strides`` are the (batch, head, row) element strides
-    the ABI expects; k/v strides are taken from the tensors.  Everything but
+    the ABI expects; k/v strides are taken from the tensors.  ``kv_len`` is
+    the ABI's field (paged: the caches' rows, 0 = unknown), ``kv_len_max`` an
+    upper bound of every sequence's KV length (0 = unknown) and
+    ``max_workgroups`` the cap on the persistent grid (0 = none).  Everything but
     the pointers depends only on the call signature, so that part of the
     parameter block (and its workspace size) is built once per signature.
     """
     dev = q.device
     key = (decode, layout, q.dtype, mask, int(num_splits), dev.index, batch, q_heads, kv_heads,
            head_dim, q_len, kv_len, tuple(q_strides), tuple(o_strides), k.stride(), v.stride(),
-           None if kt is None else (kt.stride(0), vt.stride(0), int(page_size)))
+           None if kt is None else (kt.stride(0), vt.stride(0), int(page_size)),
+           int(max_workgroups), int(kv_len_max))
     cached = _PLAN_CACHE.get(key)
     if cached is None:
         p = _fa2.Fa2Params()
@@ -107,6 +111,8 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
             p.k_table_stride, p.v_table_stride = kt.stride(0), vt.stride(0)
             p.page_size = int(page_size)
         p.softmax_scale = head_dim ** -0.5
+        p.max_workgroups = int(max_workgroups)
+        p.kv_len_max = int(kv_len_max)
         # validation needs the layout's pointers; they are overwritten per call
         _set_pointers(p, q, k, v, out, qi, kvi, kt, vt)
         with torch.cuda.device(dev):

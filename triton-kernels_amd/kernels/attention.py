@@ -24,6 +24,8 @@ call is unchanged):
   ``j <= i + Lk - Lq`` (chunked prefill); default ``"top_left"`` is the
   reference's mask (attention.py:566-569);
 * ``num_splits`` - force the split-KV factor (0 = automatic);
+* ``max_workgroups`` - cap the persistent kernel's grid (0 = one workgroup
+  per compute unit), e.g. to leave compute units to concurrent work;
 * tensors whose last dimension is not contiguous or whose rows are not
   16-byte aligned are copied to a contiguous layout first (the reference
   silently assumes contiguity, attention.py:465-514).
@@ -50,6 +52,7 @@ def flash_attention_v2(
     kv_page_size: int | None = None,
     causal_alignment: str = "top_left",
     num_splits: int = 0,
+    max_workgroups: int = 0,
 ) -> torch.Tensor:
     # --- assertion sequence of attention.py:762-834, in order -------------
     assert q.dtype == k.dtype == v.dtype
@@ -147,7 +150,9 @@ def flash_attention_v2(
             q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, q_len=M,
             kv_len=N if layout != _fa2.LAYOUT_PAGED else total_cache,
             q=q, k=k, v=v, out=out, q_strides=strides(q), o_strides=strides(out),
-            qi=qi, kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size)
+            qi=qi, kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size,
+            max_workgroups=max_workgroups,
+            kv_len_max=N if layout == _fa2.LAYOUT_PAGED else 0)
     return out
 
 

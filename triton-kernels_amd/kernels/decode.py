@@ -140,6 +140,7 @@ def _run_decode(name, q4, k, v, out4, *, layout, causal, batch, q_heads, kv_head
     enqueue(decode=True, layout=layout, mask=mask, num_splits=num_splits, batch=batch,
             q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, q_len=M, kv_len=kv_len,
             q=q4, k=k, v=v, out=dst, q_strides=abi_strides(q4), o_strides=abi_strides(dst),
-            kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size)
+            kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size,
+            kv_len_max=kt.shape[1] * kv_page_size if kt is not None else 0)
     if dst is not out4:
         out4.copy_(dst)

@@ -291,6 +291,64 @@ def make(name: str, dtype: torch.dtype | None = None, seed: int = 0,
     raise KeyError(name)
 
 
+# The reference benchmark's sweep (benchmarks/attention.py:11-55, 487-589):
+# B 16, D 128, page 16; layouts x self/cross x MHA 8/8, GQA 8/2, MQA 8/1 x
+# fp16/bf16 x causal; q_len in {128, 512}; kv_len = q_len (self) or in
+# {128, 512, 2048} (cross); causal points with q_len > kv_len skipped (:505-506).
+SWEEP_BATCH, SWEEP_D = 16, 128
+SWEEP_TOPOLOGIES = {"mha": (8, 8), "gqa": (8, 2), "mqa": (8, 1)}
+
+
+def sweep_points():
+    """(layout, attn_type, topology, dtype, causal, q_len, kv_len) in the
+    reference benchmark's loop order."""
+    pts = []
+    for layout in ("dense", "ragged", "paged"):
+        for attn in ("self", "cross"):
+            for topo in SWEEP_TOPOLOGIES:
+                for dt in (torch.float16, torch.bfloat16):
+                    for causal in (False, True):
+                        for ql in (128, 512):
+                            for kl in ((128, 512, 2048) if attn == "cross" else (ql,)):
+                                if causal and ql > kl:
+                                    continue
+                                pts.append((layout, attn, topo, dt, causal, ql, kl))
+    return pts
+
+
+def make_sweep(layout, attn_type, topology, dtype, causal, q_len, kv_len, seed=0) -> Workload:
+    """One point of the reference benchmark's sweep with seeded inputs.  Every
+    sequence has q_len queries and kv_len keys (benchmarks/attention.py:244-270);
+    paged caches are built like its build_paged_cache (pages in order, -1
+    padding, :351-431), with q laid out [B, Hq, q_len, D] as the entry point
+    reads it (the benchmark passes it transposed, :449).  kv_len is a
+    multiple of the page size at every point."""
+    gen = torch.Generator().manual_seed(seed)
+    Hq, Hkv = SWEEP_TOPOLOGIES[topology]
+    B, D = SWEEP_BATCH, SWEEP_D
+    if attn_type == "self":
+        kv_len = q_len
+    name = f"sweep {layout} {attn_type} {topology} {'causal' if causal else 'full'} q{q_len} kv{kv_len}"
+    qs = [_randn(gen, (q_len, Hq, D), dtype) for _ in range(B)]
+    ks = [_randn(gen, (kv_len, Hkv, D), dtype) for _ in range(B)]
+    vs = [_randn(gen, (kv_len, Hkv, D), dtype) for _ in range(B)]
+    common = dict(q_lens=[q_len] * B, kv_lens=[kv_len] * B, q_heads=Hq, kv_heads=Hkv,
+                  head_dim=D)
+    if layout == "dense":
+        return Workload(name, "dense", dtype, pack_dense(qs, q_len), pack_dense(ks, kv_len),
+                        pack_dense(vs, kv_len), causal, **common)
+    if layout == "ragged":
+        return Workload(name, "ragged", dtype, torch.cat(qs), torch.cat(ks), torch.cat(vs),
+                        causal, q_indptr=indptr([q_len] * B), kv_indptr=indptr([kv_len] * B),
+                        **common)
+    # equal lengths: every table row is full, as build_paged_cache's would be
+    kc, kt = paged_cache_contiguous(ks, PAGE)
+    vc, vt = paged_cache_contiguous(vs, PAGE)
+    return Workload(name, "paged", dtype, pack_dense(qs, q_len), kc, vc, causal,
+                    kv_indptr=torch.tensor([kv_len] * B, dtype=torch.int32), k_block_table=kt,
+                    v_block_table=vt, kv_page_size=PAGE, **common)
+
+
 def _make_decode(name, dt, gen) -> Workload:
     """Paged decode / speculative-decode workloads (see the module docstring)."""
     spec = name.startswith("s")
