@@ -76,10 +76,12 @@ enum fa2_status {
   FA2_ERR_SPLITS = 11,         /* num_splits out of range                       */
   FA2_ERR_HIP = 12,            /* a HIP runtime call or a launch failed         */
   FA2_ERR_TOO_LARGE = 13,      /* a size exceeds the kernels' 32-bit counters  */
-  FA2_ERR_Q_LAYOUT = 14        /* decode: the rows of the query heads sharing a
+  FA2_ERR_Q_LAYOUT = 14,       /* decode: the rows of the query heads sharing a
                                   kv head are not one strided run
                                   (q_sh != q_len * q_ss, likewise o; with M = 1
                                   pass q_ss = q_sh)                             */
+  FA2_ERR_SCRATCH = 15         /* fa2_fwd_noalloc: the call needs more scratch
+                                  than FA2_NOALLOC_SCRATCH_BYTES               */
 };
 
 /* Supported head dims (the reference accepts any power of two via
@@ -150,6 +152,22 @@ int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes);
  * (split heuristic, workspace, partial + merge launches).  Returns FA2_OK
  * or an error code; validation errors are reported before any launch. */
 int fa2_fwd(const fa2_params* p, void* stream);
+
+/* fa2_fwd for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  `p->workspace` is ignored: the ragged/paged
+ * work list and the split-KV partials live in a static device array of
+ * FA2_NOALLOC_SCRATCH_BYTES that the library holds on every device it runs on
+ * until the process ends.  Automatic splits (num_splits = 0) are reduced until
+ * the call fits that array; a call that still does not fit, or a forced
+ * num_splits that does not, returns FA2_ERR_SCRATCH before any launch.  The
+ * entry point calls no allocating routine.  Every call on one device shares
+ * that device's array: calls that overlap in time on one device (e.g. on two
+ * streams) race and give wrong results; serialise them.  Otherwise the same
+ * contract and results as fa2_fwd (bit-identical when the split factor is the
+ * same). */
+#define FA2_NOALLOC_SCRATCH_BYTES (32u << 20)
+int fa2_fwd_noalloc(const fa2_params* p, void* stream);
 
 /* Static, human-readable text for a status code. */
 const char* fa2_strerror(int status);

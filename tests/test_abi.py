@@ -36,11 +36,11 @@ def test_struct_layout_matches():
 
 def test_strerror_for_every_code():
     seen = set()
-    for code in range(15):
+    for code in range(16):
         msg = _fa2.lib().fa2_strerror(code).decode()
         assert msg and "unknown" not in msg
         seen.add(msg)
-    assert len(seen) == 15
+    assert len(seen) == 16
     assert "unknown" in _fa2.lib().fa2_strerror(999).decode()
 
 
@@ -223,3 +223,15 @@ def test_paged_split_bounded_by_pool_and_table():
     # an unknown bound keeps the old behaviour (split for parallelism)
     rc, n = rc_ws(paged_params(0))
     assert rc == 0 and n > (1 << 20)
+
+
+def test_noalloc_rejects_before_any_launch():
+    """fa2_fwd_noalloc: validation errors, and a forced split whose partials
+    exceed the static scratch, are reported before any HIP call."""
+    lib = _fa2.lib()
+    assert lib.fa2_fwd_noalloc(None, None) == 1
+    assert lib.fa2_fwd_noalloc(ctypes.byref(dense_params(head_dim=96)), None) == 6
+    # 64 splits of B2 Hq8 Lq300: 64 * 48 workgroups * 128 rows * 130 floats > 32 MiB
+    p = dense_params(num_splits=64, q=16, k=16, v=16, o=16)
+    assert rc_ws(p)[1] > _fa2.NOALLOC_SCRATCH_BYTES
+    assert lib.fa2_fwd_noalloc(ctypes.byref(p), None) == 15

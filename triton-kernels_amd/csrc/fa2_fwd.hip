@@ -432,6 +432,9 @@ extern "C" const char* fa2_strerror(int s) {
     case FA2_ERR_TOO_LARGE: return "a size exceeds the kernels' 32-bit index range";
     case FA2_ERR_Q_LAYOUT:
       return "decode: q/o head stride must equal q_len * row stride (contiguous heads)";
+    case FA2_ERR_SCRATCH:
+      return "fa2_fwd_noalloc: the call needs more than the static scratch "
+             "(FA2_NOALLOC_SCRATCH_BYTES = 32 MiB per device)";
     default: return "unknown fa2 status";
   }
 }
@@ -530,6 +533,63 @@ extern "C" int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes) {
 }
 
 extern "C" int fa2_fwd(const fa2_params* p, void* stream) { return run(p, stream, false); }
+
+// ---- fa2_fwd_noalloc: the workspace in a static device array ---------------
+//
+// Each device holds its own copy of `scratch` from the module's load until
+// the process ends.  In host code the array's name is only a stand-in for the
+// symbol: its device address comes from hipGetSymbolAddress, once per device
+// with that device current, and only that address reaches the kernels.
+// Nothing in it has to start at zero: the plan kernel writes the work list
+// and its count, and every split partial the combine reads is written by the
+// forward kernel of the same call.
+static __device__ __align__(256) unsigned char scratch[FA2_NOALLOC_SCRATCH_BYTES];
+
+namespace fa2 {
+namespace {
+
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+
+// This device's copy of `scratch`, or null if the lookup failed.
+void* scratch_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch_ptr[dev] = ptr;
+  });
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace fa2
+
+extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
+  int s = validate(p);
+  if (s != FA2_OK) return s;
+  if (empty_problem(p)) return FA2_OK;
+  constexpr size_t cap = FA2_NOALLOC_SCRATCH_BYTES;
+  fa2_params c = *p;
+  Plan pl;
+  s = make_plan(&c, &pl, c.num_splits == 0);
+  if (s != FA2_OK) return s;
+  if (pl.total > cap) {
+    if (p->num_splits != 0) return FA2_ERR_SCRATCH;
+    // fewer automatic splits until the partials fit
+    for (int sp = pl.splits - 1; sp >= 1 && pl.total > cap; --sp) {
+      c.num_splits = sp;
+      s = make_plan(&c, &pl, false);
+      if (s != FA2_OK) return s;
+    }
+    if (pl.total > cap) return FA2_ERR_SCRATCH;
+  }
+  void* ws = scratch_current_device();
+  if (!ws) return FA2_ERR_HIP;
+  c.workspace = ws;
+  c.workspace_bytes = cap;
+  return run(&c, stream, false);
+}
 
 extern "C" int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes) {
   return workspace_size(p, bytes, true);

@@ -22,9 +22,10 @@ MAX_SPLITS = 64
 ABI_VERSION = 4
 
 # Every symbol include/fa2.h declares.
-EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_strerror", "fa2_decode_workspace_size",
-           "fa2_decode_fwd", "fa2_kv_append", "fa2_kv_append_params_size", "fa2_abi_version",
-           "fa2_params_size")
+EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_fwd_noalloc", "fa2_strerror",
+           "fa2_decode_workspace_size", "fa2_decode_fwd", "fa2_kv_append",
+           "fa2_kv_append_params_size", "fa2_abi_version", "fa2_params_size")
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
 class Fa2Params(ctypes.Structure):
@@ -98,6 +99,8 @@ def lib():
             L.fa2_fwd_workspace_size.restype = ctypes.c_int
             L.fa2_fwd.argtypes = [ctypes.POINTER(Fa2Params), ctypes.c_void_p]
             L.fa2_fwd.restype = ctypes.c_int
+            L.fa2_fwd_noalloc.argtypes = [ctypes.POINTER(Fa2Params), ctypes.c_void_p]
+            L.fa2_fwd_noalloc.restype = ctypes.c_int
             L.fa2_decode_workspace_size.argtypes = [ctypes.POINTER(Fa2Params),
                                                     ctypes.POINTER(ctypes.c_size_t)]
             L.fa2_decode_workspace_size.restype = ctypes.c_int
@@ -144,6 +147,13 @@ def forward(p: Fa2Params, stream: int, decode: bool = False) -> None:
     """Enqueue ``fa2_fwd`` (or ``fa2_decode_fwd``) on the HIP stream ``stream``."""
     fn = lib().fa2_decode_fwd if decode else lib().fa2_fwd
     rc = fn(ctypes.byref(p), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise Fa2Error(rc)
+
+
+def forward_noalloc(p: Fa2Params, stream: int) -> None:
+    """Enqueue ``fa2_fwd_noalloc`` (no workspace: the library's static scratch)."""
+    rc = lib().fa2_fwd_noalloc(ctypes.byref(p), ctypes.c_void_p(stream))
     if rc != 0:
         raise Fa2Error(rc)
 

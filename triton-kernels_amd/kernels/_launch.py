@@ -73,7 +73,8 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
             q_heads: int, kv_heads: int, head_dim: int, q_len: int, kv_len: int,
             q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
             q_strides, o_strides, qi=None, kvi=None, kt=None, vt=None,
-            page_size=None, max_workgroups: int = 0, kv_len_max: int = 0) -> None:
+            page_size=None, max_workgroups: int = 0, kv_len_max: int = 0,
+            noalloc: bool = False) -> None:
     """Fill ``fa2_params`` and enqueue ``fa2_fwd`` (``decode=False``) or
     ``fa2_decode_fwd`` on torch's current stream of ``q``'s device.
 
@@ -81,7 +82,8 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
     the ABI expects; k/v strides are taken from the tensors.  ``kv_len`` is
     the ABI's field (paged: the caches' rows, 0 = unknown), ``kv_len_max`` an
     upper bound of every sequence's KV length (0 = unknown) and
-    ``max_workgroups`` the cap on the persistent grid (0 = none).  Everything but
+    ``max_workgroups`` the cap on the persistent grid (0 = none).  ``noalloc``
+    enqueues ``fa2_fwd_noalloc`` instead (no workspace; prefill only).  Everything but
     the pointers depends only on the call signature, so that part of the
     parameter block (and its workspace size) is built once per signature.
     """
@@ -132,6 +134,10 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
         torch.cuda.set_device(dev)
     try:
         stream = torch.cuda.current_stream(dev)
+        if noalloc:
+            assert not decode, "fa2_fwd_noalloc serves the prefill entry point"
+            _fa2.forward_noalloc(p, stream.cuda_stream)
+            return
         ws = None
         if ws_bytes:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
