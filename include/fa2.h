@@ -44,8 +44,20 @@ enum fa2_layout {
 enum fa2_dtype {
   FA2_DTYPE_F16 = 0,  /* fp16 MFMA, fp32 accumulation                          */
   FA2_DTYPE_BF16 = 1, /* bf16 MFMA, fp32 accumulation                          */
-  FA2_DTYPE_F32 = 2   /* operands rounded to fp16 as the reference does
-                         (attention.py:547,572,594,607,614,633), fp32 output   */
+  FA2_DTYPE_F32 = 2   /* fp32 tensors; arithmetic per fa2_arith                */
+};
+
+/* Arithmetic for fp32 tensors (fp16/bf16 tensors ignore it).
+ * FA2_ARITH_REFERENCE: what the reference entry point does - fa2_fwd as
+ *   flash_attention_v2 (operands and softmax weights rounded to fp16,
+ *   attention.py:547,572,594,607,614,633); fa2_decode_fwd as decode_attention
+ *   and speculative_decode_attention (fp32 throughout, decode.py:84,143-160,
+ *   speculative_decode.py:91,150-175).
+ * FA2_ARITH_FP32: fa2_fwd in fp32 throughout, as flash_attention_v1
+ *   (attention.py:177,196-197,225-240). */
+enum fa2_arith {
+  FA2_ARITH_REFERENCE = 0,
+  FA2_ARITH_FP32 = 1
 };
 
 /* Causal mask.  TOP_LEFT is the reference's `is_causal=True`
@@ -139,6 +151,9 @@ typedef struct fa2_params {
    * attention.py:834).  Used only to size the split-KV factor; lengths
    * always come from kv_indptr. */
   int64_t kv_len_max;
+
+  int32_t arith;      /* enum fa2_arith (fp32 tensors only)                    */
+  int32_t reserved1;  /* 0                                                      */
 } fa2_params;
 
 /* Bytes of device workspace fa2_fwd needs for `p` (0 is possible).

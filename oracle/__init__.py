@@ -185,6 +185,20 @@ def oracle_attention(q, k, v, *, is_causal=False, q_indptr=None, kv_indptr=None,
     return out
 
 
+def oracle_v1(q, k, v, *, is_causal=False, q_indptr=None, kv_indptr=None, k_block_table=None,
+              v_block_table=None, kv_page_size=None, block_n=64, scale=None):
+    """``flash_attention_v1``'s arithmetic (kernels/attention.py:164-244): the
+    same layouts, top-left mask and online softmax as v2, without split-K, with
+    q, k, v cast to fp32 (:177, :196-197, :228) and the weights P kept in fp32
+    for P.V (:225-240) - i.e. the C restatement with no rounding of operands
+    or P and one split.  (Triton's default fp32 ``tl.dot`` on NVIDIA rounds
+    its inputs to TF32; this restates the fp32 arithmetic the source asks for.)"""
+    return oracle_attention(q, k, v, is_causal=is_causal, q_indptr=q_indptr, kv_indptr=kv_indptr,
+                            k_block_table=k_block_table, v_block_table=v_block_table,
+                            kv_page_size=kv_page_size, operand_round="none", p_round="none",
+                            block_n=block_n, split_k=1, scale=scale)
+
+
 def oracle_decode(q, k, v, *, causal=False, kv_indptr=None, k_block_table=None,
                   v_block_table=None, kv_page_size=None, spec=None, operand_round="none",
                   p_round="none", block_n=64, split_k=1, scale=None, mutation=0):

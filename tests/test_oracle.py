@@ -322,3 +322,37 @@ def test_planted_mistakes_are_caught(mutation):
                        else math.inf) for o, r in zip(outs, refs))
             caught.append(err > 1e-3)
     assert any(caught), MUTATIONS[mutation]
+
+
+# ---------------------------------------------------------------------------
+# flash_attention_v1's arithmetic (oracle.oracle_v1)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("causal", CAUSAL_FLAGS)
+def test_oracle_v1_is_fp32_attention(layout, causal):
+    """fp32 inputs: the v1 restatement is within fp32 rounding of fp64 SDPA
+    (far tighter than the fp16-operand v2 restatement), on every layout."""
+    case = make_case(4, 8, 2, 64, "self", torch.float32, layout, 900 + int(causal))
+    q, k, v, lk = pack(case, layout)
+    v1 = unpack(case, layout, oracle.oracle_v1(q, k, v, is_causal=causal, **lk), lk)
+    v2 = run_oracle(case, layout, causal, rounding="f16")
+    truth = sdpa64(case, causal)
+    e1, e2 = max_err(v1, truth), max_err(v2, truth)
+    assert e1 < 2e-6, e1
+    assert e2 > 50 * e1, (e1, e2)
+
+
+def test_oracle_v1_keeps_fp32_range():
+    """Values past fp16's range: v1's arithmetic stays finite and exact to fp32,
+    v2's fp16 operands overflow (the reference's .to(float16) casts)."""
+    case = make_case(2, 4, 4, 64, "self", torch.float32, "dense", 950)
+    case.vs = [x * 1.0e5 for x in case.vs]
+    q, k, v, lk = pack(case, "dense")
+    v1 = unpack(case, "dense", oracle.oracle_v1(q, k, v, is_causal=True, **lk), lk)
+    truth = sdpa64(case, True)
+    assert all(torch.isfinite(o).all() for o in v1)
+    rel = max_err(v1, truth) / max(t.abs().max().item() for t in truth)
+    assert rel < 2e-6, rel
+    v2 = run_oracle(case, "dense", True, rounding="f16")
+    assert not all(torch.isfinite(o).all() for o in v2)

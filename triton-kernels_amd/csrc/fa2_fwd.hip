@@ -18,6 +18,7 @@
 #include "fa2_kernel_lds.h"
 #include "fa2_kernel_pp.h"
 #include "fa2_kernel_decode.h"
+#include "fa2_kernel_f32.h"
 #include "fa2_kv_append.h"
 
 // 1: fp16/bf16 with an even number of query heads per kv head run the
@@ -80,6 +81,7 @@ struct Plan {
   int64_t rows;     // query rows of one unit's sequence (packed: Hq/Hkv * M)
   int block_rows;   // rows per q-block of the launched kernel
   bool dec;         // packed fp16/bf16: the decode kernel
+  bool f32;         // fp32 arithmetic: the fp32-MFMA kernel
   bool plan;        // ragged/paged: the plan kernel orders the work list
   bool buf;         // paged: every row of the pool has a 31-bit byte offset
   int64_t max_wgs;  // cap on the persistent grid (0: none)
@@ -139,6 +141,7 @@ int validate(const fa2_params* p) {
   if (p->k_ss * eb > row_lim || p->v_ss * eb > row_lim || p->o_ss * eb > row_lim)
     return FA2_ERR_TOO_LARGE;
   if (p->max_workgroups < 0 || p->kv_len_max < 0) return FA2_ERR_BAD_SHAPE;
+  if (p->arith < FA2_ARITH_REFERENCE || p->arith > FA2_ARITH_FP32) return FA2_ERR_BAD_DTYPE;
   return FA2_OK;
 }
 
@@ -244,6 +247,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   pl->rows = p->q_len;
   pl->block_rows = kBM;
   pl->dec = false;
+  pl->f32 = p->dtype == FA2_DTYPE_F32 && p->arith == FA2_ARITH_FP32;
   pl->plan = p->layout != FA2_LAYOUT_DENSE;
   pl->part_rows = kBM;  // the two-head kernel's partial slots assume kBM
   return finish_plan(p, pl);
@@ -286,6 +290,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   // workgroup per CU); otherwise the register-staged kernel (128-row blocks)
   pl->dim = tile_dim(p->head_dim);
   pl->dec = p->dtype != FA2_DTYPE_F32 && fast_dim(p->head_dim);
+  pl->f32 = p->dtype == FA2_DTYPE_F32;  // decode's reference computes fp32 in fp32
   pl->block_rows = pl->dec ? kDecRows : kBM;
   const int64_t nqb = cdiv(pl->rows, pl->block_rows);
   pl->work_ub = nqb * p->batch;
@@ -346,6 +351,16 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
                          const_cast<int2*>(a.work), const_cast<int32_t*>(a.work_count));
   }
   const dim3 grid(pl.grid_x, pl.splits);
+  if constexpr (DT == FA2_DTYPE_F32) {
+    if (pl.f32) {
+      FA2_LAUNCH_BUF(fa2_fwd_f32_kernel, grid, dim3(kThreads));
+      if (pl.splits > 1)
+        hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
+                           dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads),
+                           0, st, a);
+      return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
+    }
+  }
   if constexpr (DT != FA2_DTYPE_F32 && (D == 64 || D == 128)) {
     if (pl.dec) {
       FA2_LAUNCH_BUF(fa2_decode_kernel, grid, dim3(kDecThreads));
@@ -410,7 +425,7 @@ int launch_dim(int64_t d, int mode, const KArgs& a, const Plan& pl, hipStream_t 
 
 using namespace fa2;
 
-extern "C" int fa2_abi_version(void) { return 4; }
+extern "C" int fa2_abi_version(void) { return 5; }
 
 extern "C" size_t fa2_params_size(void) { return sizeof(fa2_params); }
 
@@ -419,7 +434,8 @@ extern "C" const char* fa2_strerror(int s) {
     case FA2_OK: return "success";
     case FA2_ERR_NULL_POINTER: return "a required pointer is NULL";
     case FA2_ERR_BAD_LAYOUT: return "layout must be dense (0), ragged (1) or paged (2)";
-    case FA2_ERR_BAD_DTYPE: return "dtype must be f16 (0), bf16 (1) or f32 (2)";
+    case FA2_ERR_BAD_DTYPE:
+      return "dtype must be f16 (0), bf16 (1) or f32 (2), arith reference (0) or fp32 (1)";
     case FA2_ERR_BAD_MASK: return "mask must be none (0), top-left causal (1) or bottom-right causal (2)";
     case FA2_ERR_BAD_SHAPE: return "invalid shape (negative size or q_heads % kv_heads != 0)";
     case FA2_ERR_HEAD_DIM: return "unsupported head_dim (supported: 16, 32, 64, 128, 256)";

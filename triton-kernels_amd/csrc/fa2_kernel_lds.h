@@ -41,6 +41,21 @@ struct SwzGeo {
   }
 };
 
+// The same for fp32 rows (the fp32-arithmetic kernel, fa2_kernel_f32.h), D >= 64.
+template <int D>
+struct SwzGeo32 {
+  static constexpr int kNC = D / 4;  // chunks per row
+  static constexpr int kRowBytes = D * 4;
+  static constexpr int kTileBytes = kBN * kRowBytes;
+  static_assert(kNC >= 16, "fp32 rows of at least 64 dims");
+  // K is read one row per lane (16 lanes per pass): 16 rows at one chunk
+  // column go to 16 distinct 16-byte bank groups.
+  __device__ __forceinline__ static int k(int r) { return r & 15; }
+  // V is read one dim per lane, keys r (lanes 0-31) and r + 4 (lanes 32-63):
+  // the two rows' 128-byte runs land on opposite halves of the 64 banks.
+  __device__ __forceinline__ static int v(int r) { return ((r >> 2) & 1) << 3; }
+};
+
 __device__ __forceinline__ lds_char_t* to_lds(void* p) {
   return (lds_char_t*)((__attribute__((address_space(3))) uint16_t*)(uint16_t*)p);
 }
@@ -109,16 +124,45 @@ __device__ __forceinline__ lds_char_t* lds_ptr(uint32_t addr) {
 // Tile loads shared by NW waves (each issues kInstr 1 KiB instructions).
 template <int D, int MODE, bool BUF, int DT, int NW = kWaves>
 struct DirectLoader {
-  using G = SwzGeo<D>;
-  static constexpr int kEB = 2;
+  using G = std::conditional_t<DT == FA2_DTYPE_F32, SwzGeo32<D>, SwzGeo<D>>;
+  static constexpr int kEB = Elt<DT>::kBytes;
   static constexpr int kInstr = G::kNC / NW;  // 1 KiB wave instructions per tensor per tile
   static_assert(kInstr * NW == G::kNC, "tile must split evenly over the loading waves");
   static_assert(kInstr >= 1, "head dim");
+  // fp32 tiles of 64 dims also serve head_dim 16 and 32 (KArgs::dv): the
+  // chunks past dv are zero-filled, never read from memory
+  static constexpr bool kDV = DT == FA2_DTYPE_F32 && D == 64;
 
   // dense/ragged: byte offset (row * stride + swizzled chunk) of this lane's
-  // slot for instruction j, relative to the tile's first row
-  uint32_t kvo[kInstr], vvo[kInstr];
+  // slot for instruction j, relative to the tile's first row (paged: to the
+  // first row of the instruction).  fp32 tiles (kLazy) compute them when
+  // issuing instead of holding 2 * kInstr registers through the kernel.
+  static constexpr bool kLazy = DT == FA2_DTYPE_F32;
+  uint32_t kvo[kLazy ? 1 : kInstr], vvo[kLazy ? 1 : kInstr];
+  uint32_t krs, vrs;  // row strides in bytes
   int wave, lane;
+  // bit j: the source chunk this lane loads with instruction j holds data
+  // (head dims below dv); only tracked when kDV
+  uint32_t kmask, vmask;
+  __device__ __forceinline__ bool kok(int j) const { return !kDV || ((kmask >> j) & 1u); }
+  __device__ __forceinline__ bool vok(int j) const { return !kDV || ((vmask >> j) & 1u); }
+  template <bool IS_V>
+  __device__ __forceinline__ bool cok(int j) const { return IS_V ? vok(j) : kok(j); }
+
+  // byte offset of this lane's slot for instruction j: dense/ragged from
+  // the tile's first row; paged from the first row of the instruction's
+  // kRPI-row group (its page row is added by the caller)
+  template <bool IS_V>
+  __device__ __forceinline__ uint32_t offset(int j) const {
+    const int r = row_of(j);
+    const int rr = (MODE == FA2_LAYOUT_PAGED) ? lane_row() : r;
+    return rr * (IS_V ? vrs : krs) + ((slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16);
+  }
+  template <bool IS_V>
+  __device__ __forceinline__ uint32_t src_off(int j) const {
+    if constexpr (kLazy) return offset<IS_V>(j);
+    else return IS_V ? vvo[j] : kvo[j];
+  }
 
   // tile row and 16-byte slot of this lane for wave instruction j
   __device__ __forceinline__ int row_of(int j) const {
@@ -139,16 +183,21 @@ struct DirectLoader {
   __device__ __forceinline__ DirectLoader(const KArgs& a, int wv, int ln) {
     wave = wv;
     lane = ln;
-    const uint32_t krs = static_cast<uint32_t>(a.k_ss * kEB);
-    const uint32_t vrs = static_cast<uint32_t>(a.v_ss * kEB);
+    kmask = vmask = 0u;
+    krs = static_cast<uint32_t>(a.k_ss * kEB);
+    vrs = static_cast<uint32_t>(a.v_ss * kEB);
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
       const int r = row_of(j);
-      // dense/ragged: offset from the tile's first row; paged: from the first
-      // row of this instruction's kRPI-row group (its page row is added later)
-      const int rr = (MODE == FA2_LAYOUT_PAGED) ? lane_row() : r;
-      kvo[j] = rr * krs + ((slot_of() ^ G::k(r)) * 16);
-      vvo[j] = rr * vrs + ((slot_of() ^ G::v(r)) * 16);
+      if constexpr (!kLazy) {
+        kvo[j] = offset<false>(j);
+        vvo[j] = offset<true>(j);
+      }
+      if constexpr (kDV) {
+        constexpr int kPerChunk = 16 / kEB;  // elements per 16-byte chunk
+        kmask |= static_cast<uint32_t>((slot_of() ^ G::k(r)) * kPerChunk < a.dv) << j;
+        vmask |= static_cast<uint32_t>((slot_of() ^ G::v(r)) * kPerChunk < a.dv) << j;
+      }
     }
   }
 
@@ -220,8 +269,9 @@ struct DirectLoader {
         page_rsrc(a, static_cast<const char*>(src) + base * kEB, prow, kSpan, rsb);
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
-      const uint32_t off = j * kRPI * rsb + (IS_V ? vvo[j] : kvo[j]);
-      dma_buffer_x4(rsrc, ldst + j * 1024, n0 + j * kRPI + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+      const uint32_t off = j * kRPI * rsb + src_off<IS_V>(j);
+      dma_buffer_x4(rsrc, ldst + j * 1024,
+                    (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
     }
   }
 
@@ -260,9 +310,9 @@ struct DirectLoader {
         const u32x4 rsrc = page_rsrc(a, pool, prow, kSpan, rsb);
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
-          const uint32_t off = j * kRPI * rsb + (IS_V ? vvo[j] : kvo[j]);
+          const uint32_t off = j * kRPI * rsb + src_off<IS_V>(j);
           dma_buffer_x4(rsrc, ldst + j * 1024,
-                        n0 + j * kRPI + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+                        (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
         }
       } else if (a.page_size % kRPI == 0) {
 #pragma unroll
@@ -270,8 +320,9 @@ struct DirectLoader {
           const int n0 = k0 + (wave * kInstr + j) * kRPI;  // uniform
           const int prow = paged_row_uniform(a, tbl, ts, w.b, min(n0, w.Lk - 1));
           const u32x4 rsrc = page_rsrc(a, pool, prow, kRPI, rsb);
-          const uint32_t off = IS_V ? vvo[j] : kvo[j];
-          dma_buffer_x4(rsrc, ldst + j * 1024, n0 + lane_row() < w.Lk ? off : 0xFFFFFF00u);
+          const uint32_t off = src_off<IS_V>(j);
+          dma_buffer_x4(rsrc, ldst + j * 1024,
+                        (n0 + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
         }
       } else if constexpr (BUF) {
         const u32x4 rsrc = rsrc_words(pool, IS_V ? a.pool_bytes_v : a.pool_bytes_k);
@@ -282,7 +333,8 @@ struct DirectLoader {
           const int nc = min(n, w.Lk - 1);
           const uint32_t prow = static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
           const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
-          dma_buffer_x4(rsrc, ldst + j * 1024, n < w.Lk ? prow * rsb + col : 0xFFFFFF00u);
+          dma_buffer_x4(rsrc, ldst + j * 1024,
+                        (n < w.Lk && cok<IS_V>(j)) ? prow * rsb + col : 0xFFFFFF00u);
         }
       } else {
 #pragma unroll
@@ -290,7 +342,10 @@ struct DirectLoader {
           const int r = row_of(j);
           const int n = min(k0 + r, w.Lk - 1);  // clamped: finite data, masked later
           const int64_t prow = paged_row(tbl, ts, w.b, n, a.page_size);
-          const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
+          // (a chunk past dv reads the row's first chunk instead: finite data
+          // that meets zero q dims, or V columns that are never stored)
+          const uint32_t col =
+              cok<IS_V>(j) ? (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16 : 0u;
           dma_global_x4(pool + prow * rs * kEB + col, ldst + j * 1024);
         }
       }
@@ -300,7 +355,9 @@ struct DirectLoader {
       const u32x4 rsrc = rsrc_words(
           static_cast<const char*>(src) + (base + static_cast<int64_t>(k0) * rs) * kEB, lim);
 #pragma unroll
-      for (int j = 0; j < kInstr; ++j) dma_buffer_x4(rsrc, ldst + j * 1024, IS_V ? vvo[j] : kvo[j]);
+      for (int j = 0; j < kInstr; ++j)
+        dma_buffer_x4(rsrc, ldst + j * 1024,
+                      cok<IS_V>(j) ? src_off<IS_V>(j) : 0xFFFFFF00u);
     }
   }
 };

@@ -17,9 +17,10 @@ LIB_PATH = os.path.join(_HERE, "libfa2.so")
 LAYOUT_DENSE, LAYOUT_RAGGED, LAYOUT_PAGED = 0, 1, 2
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 MASK_NONE, MASK_TOP_LEFT, MASK_BOTTOM_RIGHT = 0, 1, 2
+ARITH_REFERENCE, ARITH_FP32 = 0, 1
 MAX_SPLITS = 64
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every symbol include/fa2.h declares.
 EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_fwd_noalloc", "fa2_strerror",
@@ -62,6 +63,8 @@ class Fa2Params(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("kv_len_max", ctypes.c_int64),
+        ("arith", ctypes.c_int32),
+        ("reserved1", ctypes.c_int32),
     ]
 
 

@@ -54,6 +54,17 @@ def flash_attention_v2(
     num_splits: int = 0,
     max_workgroups: int = 0,
 ) -> torch.Tensor:
+    return _attention(q, k, v, is_causal=is_causal, q_indptr=q_indptr, kv_indptr=kv_indptr,
+                      k_block_table=k_block_table, v_block_table=v_block_table,
+                      kv_page_size=kv_page_size, causal_alignment=causal_alignment,
+                      num_splits=num_splits, max_workgroups=max_workgroups,
+                      arith=_fa2.ARITH_REFERENCE)
+
+
+def _attention(q, k, v, *, is_causal, q_indptr, kv_indptr, k_block_table, v_block_table,
+               kv_page_size, causal_alignment, num_splits, max_workgroups, arith):
+    """The shared body of both entry points; ``arith`` is the fa2_arith of
+    fp32 tensors (v2: the reference's fp16 rounding; v1: fp32)."""
     # --- assertion sequence of attention.py:762-834, in order -------------
     assert q.dtype == k.dtype == v.dtype
     assert q.device == k.device == v.device
@@ -152,7 +163,7 @@ def flash_attention_v2(
             q=q, k=k, v=v, out=out, q_strides=strides(q), o_strides=strides(out),
             qi=qi, kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size,
             max_workgroups=max_workgroups,
-            kv_len_max=N if layout == _fa2.LAYOUT_PAGED else 0)
+            kv_len_max=N if layout == _fa2.LAYOUT_PAGED else 0, arith=arith)
     return out
 
 
@@ -173,11 +184,14 @@ def flash_attention_v1(
 
     The reference's v1 has the same signature, the same assertion sequence
     (:261-330, identical to v2's :762-834), the same layouts, head map,
-    top-left causal mask and softmax scale as v2; it differs only in its
-    Triton schedule (a persistent kernel without split-K).  Both produce the
-    same attention, so v1 is served by the same gfx950 kernels as
-    :func:`flash_attention_v2`, with v1's keyword set.
+    top-left causal mask and softmax scale as v2.  Its arithmetic differs:
+    q, k and v are cast to fp32 and the softmax weights stay fp32 (:177,
+    196-197, 225-240), where v2 computes in fp16 (:547-633).  fp32 tensors
+    therefore run the fp32-MFMA kernel here (fa2_arith FP32); fp16/bf16
+    tensors are exact in either and run v2's kernels, whose softmax weights
+    are rounded to the tensor type for the P.V product.
     """
-    return flash_attention_v2(q, k, v, is_causal=is_causal, q_indptr=q_indptr,
-                              kv_indptr=kv_indptr, k_block_table=k_block_table,
-                              v_block_table=v_block_table, kv_page_size=kv_page_size)
+    return _attention(q, k, v, is_causal=is_causal, q_indptr=q_indptr, kv_indptr=kv_indptr,
+                      k_block_table=k_block_table, v_block_table=v_block_table,
+                      kv_page_size=kv_page_size, causal_alignment="top_left", num_splits=0,
+                      max_workgroups=0, arith=_fa2.ARITH_FP32)
