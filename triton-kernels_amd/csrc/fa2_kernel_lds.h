@@ -69,22 +69,26 @@ __device__ __forceinline__ lds_char_t* to_lds(void* p) {
 // buffer is not read before the next barrier (volatile asm is not moved
 // across it), the source K/V is never written, and without the clobber the
 // block-table reads stay eligible for the scalar unit.
+//
+// M0 (the LDS destination of these loads) is an operand of the statement, so
+// the compiler writes it and knows it is read; its hazard recognizer does not
+// look inside inline asm, so the wait states gfx950 needs before the load are
+// written out (the counts hipcc emits around the equivalent builtins):
+//   * a VALU write of an SGPR (v_readfirstlane / v_readlane, which produce
+//     the descriptor words and restore spilled SGPRs) followed by a vector
+//     memory instruction that reads that SGPR: 5 wait states (s_nop 4);
+//   * an SALU write of M0 followed by a load to LDS: 1 (s_nop 0).
 __device__ __forceinline__ void dma_buffer_x4(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
-      :
-      : "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))), "v"(voff), "s"(rsrc)
-      : "m0");
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
 }
 
 __device__ __forceinline__ void dma_global_x4(const void* gptr, uint32_t lds_addr) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "global_load_lds_dwordx4 %1, off"
-      :
-      : "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))), "v"(gptr)
-      : "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gptr), "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
 }
 
 // One 32-bit read of read-only global memory at a wave-uniform address through
