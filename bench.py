@@ -239,6 +239,11 @@ def main(argv=None):
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--windows", type=int, default=5,
                     help="event-pair windows over the timed steps (median of their means)")
+    ap.add_argument("--pool-gib", type=float, default=0.0,
+                    help="paged configs: move the pages into K and V pools of at least this "
+                         "many GiB each (pages near the top, past 2 GiB from 3.2 GiB on for c4); "
+                         "the output is checked "
+                         "bitwise against the compact pool's")
     ap.add_argument("--sweep", action="store_true",
                     help="time the reference benchmark's sweep of shapes instead")
     ap.add_argument("--sweep-out", default=None, help="JSON lines of the sweep")
@@ -300,6 +305,18 @@ def main(argv=None):
         return sweep(args)
     dt = DTYPES[args.dtype] if args.dtype else None
     w_cpu = W.make(args.config, dtype=dt, causal_alignment=args.alignment)
+    pool_check = None
+    if args.pool_gib > 0:
+        if w_cpu.layout != "paged":
+            print("bench.py: --pool-gib applies to paged configs only", file=sys.stderr)
+            return 2
+        compact = w_cpu.to(dev)
+        fn0 = {"prefill": flash_attention_v2, "decode": decode_attention,
+               "speculative": speculative_decode_attention}[compact.kind]
+        ref_out = fn0(compact.q, compact.k, compact.v, **compact.kwargs()).cpu()
+        del compact
+        torch.cuda.empty_cache()
+        w_cpu = W.spread_pool(w_cpu, args.pool_gib)
     w = w_cpu.to(dev)
     kw = w.kwargs()
     fl = W.flops(w)
@@ -319,6 +336,15 @@ def main(argv=None):
         def step():
             return fn(w.q, w.k, w.v, **kw)
 
+    if args.pool_gib > 0:
+        out = step()
+        torch.cuda.synchronize()
+        pool_check = {"pool_gib_each": round(w.k.numel() * w.k.element_size() / 2**30, 3),
+                      "pages_past_2gib": int(((w.k_block_table.long() * w.kv_page_size *
+                                               w.k[0].numel() * w.k.element_size())
+                                              >= 2**31).sum().item()),
+                      "output_equals_compact_pool": bool(torch.equal(out.cpu(), ref_out))}
+        del out
     print(f"bench: {DESCR[args.config]} {DTYPE_NAME[w.dtype]} warmup={args.warmup} "
           f"steps={args.steps}", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
@@ -379,6 +405,7 @@ def main(argv=None):
             "gflop_per_step": round(fl / 1e9, 3),
             "algorithmic_mb_per_step": round(nbytes / 1e6, 2),
             "l2_mall_flushed": bool(args.flush),
+            **({"large_pool": pool_check} if pool_check else {}),
             "parallelism": "single GPU",
         },
         "roofline": {

@@ -291,6 +291,36 @@ def make(name: str, dtype: torch.dtype | None = None, seed: int = 0,
     raise KeyError(name)
 
 
+def spread_pool(w: Workload, gib: float, seed: int = 1) -> Workload:
+    """The same paged workload with its pages moved into pools of at least
+    `gib` GiB each: every used page goes to a random slot among the pool's
+    last 4x-its-page-count slots (all past the 2 GiB mark once `gib` exceeds 2
+    plus that span), the tables are remapped, the other slots hold zeros.  Every sequence sees the same K/V rows in the same
+    order, so the output must equal the compact pool's bit for bit."""
+    assert w.layout == "paged"
+    row_bytes = w.k[0].numel() * w.k.element_size()
+    page_bytes = w.kv_page_size * row_bytes
+    old_pages = w.k.shape[0] // w.kv_page_size
+    pages = max(old_pages, -(-int(gib * (1 << 30)) // page_bytes))
+    gen = torch.Generator().manual_seed(seed)
+
+    def move(cache, table):
+        span = min(pages, 4 * old_pages)
+        dst = pages - span + torch.randperm(span, generator=gen)[:old_pages]
+        big = torch.zeros((pages * w.kv_page_size,) + tuple(cache.shape[1:]), dtype=cache.dtype)
+        big.view(pages, w.kv_page_size, -1)[dst] = cache.view(old_pages, w.kv_page_size, -1)
+        t = table.clone().long()
+        used = t >= 0
+        t[used] = dst[t[used]]
+        return big, t.to(torch.int32)
+
+    kc, kt = move(w.k, w.k_block_table)
+    vc, vt = move(w.v, w.v_block_table)
+    out = Workload(**{f: getattr(w, f) for f in w.__dataclass_fields__})
+    out.k, out.v, out.k_block_table, out.v_block_table = kc, vc, kt, vt
+    return out
+
+
 # The reference benchmark's sweep (benchmarks/attention.py:11-55, 487-589):
 # B 16, D 128, page 16; layouts x self/cross x MHA 8/8, GQA 8/2, MQA 8/1 x
 # fp16/bf16 x causal; q_len in {128, 512}; kv_len = q_len (self) or in
