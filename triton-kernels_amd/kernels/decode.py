@@ -17,11 +17,14 @@ so each K/V row is streamed from HBM once per kv head, and the KV sweep is
 split across workgroups with a log-sum-exp combine (the reference's split +
 merge, decode.py:22-200).  No CPU or PyTorch fallback.
 
-Numerics: fp16/bf16 scores and P.V on MFMA with fp32 accumulation and fp32
-softmax statistics (the reference upcasts to fp32, decode.py:97-141, and
-computes on CUDA cores); fp32 inputs are rounded to fp16 for the MFMA, as
-this build's flash_attention_v2 does.  Both are within the reference test's
-tolerances (tests/test_decode.py:20-30).
+Numerics: the reference loads every dtype into fp32 and computes in fp32
+(decode.py:84, 92-160).  fp32 tensors do the same here, on the fp32 MFMA
+(``v_mfma_f32_32x32x2_f32``: fp32 operands and softmax weights), so values
+past fp16's range stay finite.  fp16/bf16 tensors are exact in fp32 and run on
+the 16-bit MFMA with fp32 accumulation and fp32 softmax statistics; only P is
+rounded to the tensor type for the P.V product.  Both are within the
+reference test's tolerances (tests/test_decode.py:20-30) and the GPU tests'
+strict bar against the reference's fp32 arithmetic.
 """
 
 from __future__ import annotations
