@@ -24,6 +24,8 @@ def rows_ok(t: torch.Tensor) -> bool:
     """Last dim contiguous and every row start 16-byte aligned."""
     if t.numel() == 0:
         return True
+    if t.is_contiguous():  # every stride is a multiple of the row length
+        return t.data_ptr() % 16 == 0 and (t.shape[-1] * t.element_size()) % 16 == 0
     if t.stride(-1) != 1:
         return False
     es = t.element_size()
@@ -62,6 +64,17 @@ def check_dtype_and_dim(name: str, dtype, head_dim: int) -> None:
     if head_dim not in SUPPORTED_HEAD_DIMS:
         raise ValueError(f"{name}: head_dim {head_dim} not supported "
                          f"(supported: {SUPPORTED_HEAD_DIMS})")
+
+
+# torch's current HIP stream of a device as a raw handle (the Stream object
+# is only built when a workspace has to be recorded on it)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_handle(dev) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(dev.index)
+    return torch.cuda.current_stream(dev).cuda_stream
 
 
 # call signature -> (static bytes of the parameter block, workspace bytes)
@@ -135,18 +148,18 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
         prev = torch.cuda.current_device()
         torch.cuda.set_device(dev)
     try:
-        stream = torch.cuda.current_stream(dev)
+        handle = _stream_handle(dev)
         if noalloc:
             assert not decode, "fa2_fwd_noalloc serves the prefill entry point"
-            _fa2.forward_noalloc(p, stream.cuda_stream)
+            _fa2.forward_noalloc(p, handle)
             return
         ws = None
         if ws_bytes:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
-        _fa2.forward(p, stream.cuda_stream, decode)
+        _fa2.forward(p, handle, decode)
         if ws is not None:
-            ws.record_stream(stream)
+            ws.record_stream(torch.cuda.current_stream(dev))
     finally:
         if switch:
             torch.cuda.set_device(prev)

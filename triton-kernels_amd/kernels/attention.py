@@ -141,8 +141,8 @@ def _attention(q, k, v, *, is_causal, q_indptr, kv_indptr, k_block_table, v_bloc
     q = prep(q)
     k = prep(k)
     v = prep(v)
-    out = torch.empty_like(q)
-    if not rows_ok(out):
+    out = torch.empty_like(q)  # contiguous and aligned when q is (the common case)
+    if not q.is_contiguous() and not rows_ok(out):
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
     dev = q.device
