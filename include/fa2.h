@@ -153,7 +153,14 @@ typedef struct fa2_params {
   int64_t kv_len_max;
 
   int32_t arith;      /* enum fa2_arith (fp32 tensors only)                    */
-  int32_t reserved1;  /* 0                                                      */
+
+  /* fa2_decode_fwd, fp16/bf16: polls after which a wait of the decode
+   * kernel's producer/consumer ring gives up (0 = the library's bound, about
+   * 5 ms).  A wait that gives up poisons its rows with NaN and counts in
+   * fa2_decode_wait_giveups().  Only tests set it, to exercise that path from
+   * the host.  No counterpart in the reference, whose decode kernels do not
+   * synchronise waves. */
+  int32_t decode_spin_cap;
 } fa2_params;
 
 /* Bytes of device workspace fa2_fwd needs for `p` (0 is possible).
@@ -224,6 +231,15 @@ int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes);
  * reported before any launch.  No allocation, no host synchronisation. */
 int fa2_decode_fwd(const fa2_params* p, void* stream);
 
+/* Number of bounded waits in the fp16/bf16 decode kernel that gave up on the
+ * current device since the library was loaded (or since the last reset),
+ * into *count; reset != 0 sets it back to 0.  A wait gives up only if a
+ * ring counter never reaches its target (never, in a correct run) or under a
+ * tiny decode_spin_cap; the rows of such a workgroup are then NaN.
+ * Synchronous (a device-to-host copy).  No counterpart in the reference: a
+ * diagnostic for callers that want to assert no wait ever gave up. */
+int fa2_decode_wait_giveups(uint32_t* count, int reset);
+
 /* ---- paged KV-cache writer -------------------------------------------------
  *
  * Writes new K/V rows into the paged caches the attention entry points read.
@@ -274,7 +290,7 @@ int fa2_kv_append(const fa2_kv_append_params* p, void* stream);
 /* sizeof(fa2_kv_append_params) as compiled into the library (binding check). */
 size_t fa2_kv_append_params_size(void);
 
-/* Version of this ABI (bumped on any change to fa2_params).  No counterpart
+/* Version of this ABI (bumped on any change to fa2_params or the entry points).  No counterpart
  * in the reference: lets a binding refuse a library it was not written for. */
 int fa2_abi_version(void);
 

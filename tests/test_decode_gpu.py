@@ -270,3 +270,44 @@ def test_assertions_match_reference():
     with pytest.raises(ValueError):
         decode_attention(q, torch.randn((2, 3, 10, 64), device=DEV, dtype=torch.float16),
                          torch.randn((2, 3, 10, 64), device=DEV, dtype=torch.float16))
+
+
+def test_bounded_wait_giveup_is_never_silent():
+    """The decode kernel's producer/consumer ring waits are bounded; a wait
+    that gives up must show.  Forced from the host with decode_spin_cap = 1
+    (one poll), every workgroup whose waits gave up writes NaN rows and is
+    counted by fa2_decode_wait_giveups; the others stay equal to the normal
+    call.  With the library's bound no wait gives up and the count stays 0."""
+    from kernels import _fa2
+    from kernels.decode import _run_decode
+    g = torch.Generator(device=DEV).manual_seed(777)
+    B, QH, KVH, D, N = 4, 16, 2, 128, 4096
+    q = torch.randn(B, QH, D, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B, KVH, N, D, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(B, KVH, N, D, generator=g, device=DEV).to(torch.bfloat16)
+
+    def call(cap):
+        out = torch.empty_like(q)
+        _run_decode("decode_attention", q.unsqueeze(2), k, v, out.unsqueeze(2),
+                    layout=_fa2.LAYOUT_DENSE, causal=False, batch=B, q_heads=QH, kv_heads=KVH,
+                    head_dim=D, kv_indptr=None, k_block_table=None, v_block_table=None,
+                    kv_page_size=None, num_splits=1, decode_spin_cap=cap)
+        torch.cuda.synchronize()
+        return out
+
+    _fa2.decode_wait_giveups(reset=True)
+    ref = call(0)
+    assert _fa2.decode_wait_giveups(reset=True) == 0
+    assert torch.isfinite(ref).all()
+    forced = call(1)
+    n = _fa2.decode_wait_giveups(reset=True)
+    # one workgroup per (sequence, kv head) here: its QH / KVH query heads
+    units = forced.view(B, KVH, QH // KVH, D)
+    nan_units = units.isnan().flatten(2).all(-1)
+    finite_units = torch.isfinite(units).flatten(2).all(-1)
+    assert n >= 1, "one poll never gave up: the forced path did not run"
+    assert int(nan_units.sum()) == n
+    assert bool((nan_units | finite_units).all())
+    same = ref.view(B, KVH, QH // KVH, D)[finite_units]
+    assert torch.equal(units[finite_units], same)
+    assert torch.isfinite(call(0)).all() and _fa2.decode_wait_giveups() == 0

@@ -114,6 +114,7 @@ struct KArgs {
   // read as zeros (they add nothing to Q.K^T and give zero output columns)
   // and are never stored.
   int32_t dv;
+  int32_t spin_cap;  // polls after which a decode-kernel ring wait gives up
   // Two-head kernel on MHA (Hq == Hkv, one split): a unit is a pair
   // of q-blocks (2k, 2k + 1) of one head, one per wave group, both over the
   // KV tiles of block 2k + 1 (the extra tiles are fully masked for block 2k

@@ -142,6 +142,7 @@ int validate(const fa2_params* p) {
     return FA2_ERR_TOO_LARGE;
   if (p->max_workgroups < 0 || p->kv_len_max < 0) return FA2_ERR_BAD_SHAPE;
   if (p->arith < FA2_ARITH_REFERENCE || p->arith > FA2_ARITH_FP32) return FA2_ERR_BAD_DTYPE;
+  if (p->decode_spin_cap < 0) return FA2_ERR_BAD_SHAPE;
   return FA2_OK;
 }
 
@@ -425,7 +426,7 @@ int launch_dim(int64_t d, int mode, const KArgs& a, const Plan& pl, hipStream_t 
 
 using namespace fa2;
 
-extern "C" int fa2_abi_version(void) { return 5; }
+extern "C" int fa2_abi_version(void) { return 6; }
 
 extern "C" size_t fa2_params_size(void) { return sizeof(fa2_params); }
 
@@ -532,6 +533,7 @@ int run(const fa2_params* p, void* stream, bool packed) {
   a.part_rows = pl.part_rows;
   a.pack_m = packed ? static_cast<int32_t>(p->q_len) : 0;
   a.dv = static_cast<int32_t>(p->head_dim);
+  a.spin_cap = p->decode_spin_cap > 0 ? p->decode_spin_cap : kDecSpinCap;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (p->dtype) {
@@ -612,6 +614,22 @@ extern "C" int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes) {
 }
 
 extern "C" int fa2_decode_fwd(const fa2_params* p, void* stream) { return run(p, stream, true); }
+
+extern "C" int fa2_decode_wait_giveups(uint32_t* count, int reset) {
+  if (!count) return FA2_ERR_NULL_POINTER;
+  unsigned int v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(fa2::g_decode_giveups), sizeof(v), 0,
+                          hipMemcpyDeviceToHost) != hipSuccess)
+    return FA2_ERR_HIP;
+  *count = v;
+  if (reset) {
+    const unsigned int z = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(fa2::g_decode_giveups), &z, sizeof(z), 0,
+                          hipMemcpyHostToDevice) != hipSuccess)
+      return FA2_ERR_HIP;
+  }
+  return FA2_OK;
+}
 
 extern "C" size_t fa2_kv_append_params_size(void) { return sizeof(fa2_kv_append_params); }
 

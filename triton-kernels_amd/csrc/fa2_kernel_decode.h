@@ -24,9 +24,12 @@
 //   * each consumer keeps its own running max / sum / O^T over its half of
 //     the keys; the two halves are merged through LDS at the end.
 // The counters live in LDS and only grow; a wave polls them with s_sleep
-// between reads, and every poll gives up after kDecSpinCap reads, so a wave
-// cannot wait forever even if a counter were wrong (the result would then
-// be wrong, which the parity tests see, instead of a hung GPU).
+// between reads, and every poll gives up after KArgs::spin_cap reads
+// (kDecSpinCap unless a test lowers it), so a wave cannot wait forever even
+// if a counter were wrong.  A workgroup in which any wait gave up writes NaN
+// for all its rows (output or split partials, which the combine turns into
+// NaN rows) and adds 1 to g_decode_giveups, which fa2_decode_wait_giveups()
+// reads: a wrong result is never silent.
 #pragma once
 
 #include "fa2_kernel_lds.h"
@@ -37,6 +40,10 @@ constexpr int kDecRows = 64;      // unit rows per workgroup (two chunks of 32)
 constexpr int kDecWaves = 8;      // 4 consumers + 4 producers
 constexpr int kDecThreads = 64 * kDecWaves;
 constexpr int kDecSpinCap = 1 << 16;  // ~5 ms of polling; real waits are microseconds
+
+// Workgroups of the decode kernel in which a bounded wait gave up (one
+// counter per device, read and reset by the host).
+__device__ unsigned int g_decode_giveups;
 
 // A ring slot holds kSub 64-key sub-tiles of K, then the same of V, so that
 // one slot is 32 KiB at both head dims (the per-slot handshake costs the
@@ -78,13 +85,19 @@ __device__ __forceinline__ void wait_tiles_after(int n) {
 
 typedef __attribute__((address_space(3))) int lds_int_t;
 
-// Wait until the LDS counter reaches `target` (bounded, see above).
-__device__ __forceinline__ void lds_wait_geq(lds_int_t* c, int target) {
-  for (int n = 0; n < kDecSpinCap; ++n) {
-    if (__builtin_amdgcn_readfirstlane(*(volatile lds_int_t*)c) >= target) break;
+// Wait until the LDS counter reaches `target`, at most `cap` polls (see
+// above); false if the wait gave up.
+__device__ __forceinline__ bool lds_wait_geq(lds_int_t* c, int target, int cap) {
+  bool ok = false;
+  for (int n = 0; n < cap; ++n) {
+    if (__builtin_amdgcn_readfirstlane(*(volatile lds_int_t*)c) >= target) {
+      ok = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
   asm volatile("" ::: "memory");  // later LDS reads stay after the poll
+  return ok;
 }
 
 // Add 1 to an LDS counter once per wave, after this wave's earlier LDS
@@ -107,7 +120,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
   constexpr int L = NS - 1;  // tiles a producer keeps in flight
 
   __shared__ __attribute__((aligned(1024))) char lds[DG::kLdsBytes];
-  __shared__ int counters[2 * NS];  // ready[NS] then done[NS]
+  __shared__ int counters[2 * NS + 1];  // ready[NS], done[NS], a wait gave up
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -135,7 +148,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
 
   lds_int_t* ready = (lds_int_t*)((__attribute__((address_space(3))) int*)counters);
   lds_int_t* done = ready + NS;
-  if (tid < 2 * NS) ready[tid] = 0;
+  lds_int_t* gave_up = done + NS;
+  if (tid < 2 * NS + 1) ready[tid] = 0;
+  bool waits_ok = true;  // every bounded wait of this wave reached its target
   __syncthreads();
 
   f32x16 o[DB];
@@ -165,7 +180,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
     }
     for (int i = 0; i < T; ++i) {
       // slot i % NS held tile i - NS: wait until every active consumer is done
-      if (i >= NS) lds_wait_geq(done + i % NS, nact * (i / NS));
+      if (i >= NS) waits_ok &= lds_wait_geq(done + i % NS, nact * (i / NS), a.spin_cap);
       char* sl = slot(i);
       const int k0 = (t_begin + i) * DG::kKeys;
       if (pre) {
@@ -238,7 +253,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
     }
 
     for (int i = 0; i < T; ++i) {
-      lds_wait_geq(ready + i % NS, 4 * (i / NS + 1));  // all four producers' parts
+      // all four producers' parts
+      waits_ok &= lds_wait_geq(ready + i % NS, 4 * (i / NS + 1), a.spin_cap);
 #pragma unroll
       for (int u = 0; u < SUB; ++u) {
       const lds_char_t* kl = to_lds(slot(i)) + u * G::kTileBytes;
@@ -325,7 +341,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
   static_assert(2 * kMergeChunk <= DG::kLdsBytes, "merge area");
   static_assert(2 * OStage<D>::kBytes <= DG::kLdsBytes, "output staging");
   // (producers take part in these barriers and do no merge work)
+  if (!waits_ok && lane == 0) *(volatile lds_int_t*)gave_up = 1;
   __syncthreads();  // every wave is done with the ring
+  const bool poisoned = *(volatile lds_int_t*)gave_up != 0;
+  if (poisoned && tid == 0) __hip_atomic_fetch_add(&g_decode_giveups, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
   typedef __attribute__((address_space(3))) float lds_float_t;
   char* mc = lds + rc * kMergeChunk;
   lds_float_t* mm = (lds_float_t*)to_lds(mc);  // m[2][32], l[2][32]
@@ -363,6 +383,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
   }
   __syncthreads();  // the merge area is reused for the output staging
   if (!cons || kh != 0) return;
+  if (poisoned) {  // a wait gave up: these rows may have read an unfinished tile
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[d][j] = __builtin_nanf("");
+    l_sum = 1.f;
+  }
 
   const int wq_first = q0 + rc * kWaveRows;
   if (S == 1) {

@@ -20,11 +20,12 @@ MASK_NONE, MASK_TOP_LEFT, MASK_BOTTOM_RIGHT = 0, 1, 2
 ARITH_REFERENCE, ARITH_FP32 = 0, 1
 MAX_SPLITS = 64
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every symbol include/fa2.h declares.
 EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_fwd_noalloc", "fa2_strerror",
-           "fa2_decode_workspace_size", "fa2_decode_fwd", "fa2_kv_append",
+           "fa2_decode_workspace_size", "fa2_decode_fwd", "fa2_decode_wait_giveups",
+           "fa2_kv_append",
            "fa2_kv_append_params_size", "fa2_abi_version", "fa2_params_size")
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -64,7 +65,7 @@ class Fa2Params(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("kv_len_max", ctypes.c_int64),
         ("arith", ctypes.c_int32),
-        ("reserved1", ctypes.c_int32),
+        ("decode_spin_cap", ctypes.c_int32),
     ]
 
 
@@ -109,6 +110,8 @@ def lib():
             L.fa2_decode_workspace_size.restype = ctypes.c_int
             L.fa2_decode_fwd.argtypes = [ctypes.POINTER(Fa2Params), ctypes.c_void_p]
             L.fa2_decode_fwd.restype = ctypes.c_int
+            L.fa2_decode_wait_giveups.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_int]
+            L.fa2_decode_wait_giveups.restype = ctypes.c_int
             L.fa2_kv_append.argtypes = [ctypes.POINTER(KvAppendParams), ctypes.c_void_p]
             L.fa2_kv_append.restype = ctypes.c_int
             L.fa2_kv_append_params_size.argtypes = []
@@ -152,6 +155,17 @@ def forward(p: Fa2Params, stream: int, decode: bool = False) -> None:
     rc = fn(ctypes.byref(p), ctypes.c_void_p(stream))
     if rc != 0:
         raise Fa2Error(rc)
+
+
+def decode_wait_giveups(reset: bool = False) -> int:
+    """Workgroups of the fp16/bf16 decode kernel on the current device whose
+    bounded ring waits gave up (their rows are NaN); ``reset`` zeroes the
+    count.  Synchronous."""
+    n = ctypes.c_uint32(0)
+    rc = lib().fa2_decode_wait_giveups(ctypes.byref(n), 1 if reset else 0)
+    if rc != 0:
+        raise Fa2Error(rc)
+    return n.value
 
 
 def forward_noalloc(p: Fa2Params, stream: int) -> None:
