@@ -247,6 +247,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            kBufferFlags);
 }
 
+// The same descriptor from wave-uniform values that the compiler may hold in
+// VGPRs: every word goes through v_readfirstlane, so each buffer instruction
+// takes it from SGPRs directly.  (A descriptor the compiler believes
+// divergent is wrapped in a waterfall loop per instruction, which also
+// serialises every store behind its own LDS read.)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_uniform(const void* base,
+                                                                    uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b)));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t n = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(bytes)));
+  void* p = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)n, kBufferFlags);
+}
+
 // ---------------------------------------------------------------------------
 // Work decoding: workgroup id -> (sequence, head, q-block) and addressing.
 // ---------------------------------------------------------------------------

@@ -443,11 +443,18 @@ __device__ __forceinline__ void store_o_staged_buf(const f32x16 (&o)[D / 32], fl
             (u32x2){pack2<BF>(o[d][g * 4 + 0] * inv, o[d][g * 4 + 1] * inv),
                     pack2<BF>(o[d][g * 4 + 2] * inv, o[d][g * 4 + 3] * inv)};
     }
+    // all reads of the pass first, then the stores back to back
+    constexpr int kIt = kWaveRows / kRowsPerRead;
+    u32x4 v[kIt];
 #pragma unroll
-    for (int it = 0; it < kWaveRows / kRowsPerRead; ++it) {
+    for (int it = 0; it < kIt; ++it) {
       const int r = it * kRowsPerRead + lane / kChunks;
-      const u32x4 v = *(const lds_u32x4_t*)(st + r * kS + ch * 16);
-      __builtin_amdgcn_raw_buffer_store_b128(v, out, r * rs + (p * DP + ch * 8) * 2, 0, 0);
+      v[it] = *(const lds_u32x4_t*)(st + r * kS + ch * 16);
+    }
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int r = it * kRowsPerRead + lane / kChunks;
+      __builtin_amdgcn_raw_buffer_store_b128(v[it], out, r * rs + (p * DP + ch * 8) * 2, 0, 0);
     }
   }
 }
