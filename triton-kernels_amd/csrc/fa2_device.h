@@ -449,7 +449,7 @@ struct TileLoader {
     if constexpr (BUF) {
       if constexpr (MODE == FA2_LAYOUT_PAGED) {
         const __amdgpu_buffer_rsrc_t rs =
-            make_rsrc(static_cast<const char*>(a.k) + w.k_base * kEB, a.pool_bytes_k);
+            make_rsrc_uniform(static_cast<const char*>(a.k) + w.k_base * kEB, a.pool_bytes_k);
 #pragma unroll
         for (int p = 0; p < kKPasses; ++p) {
           const int n = k0 + krow0 + p * kRowsPerPass;
@@ -462,7 +462,7 @@ struct TileLoader {
         const uint32_t rsb = static_cast<uint32_t>(a.k_ss * kEB);
         // the descriptor covers this tile's rows inside the sequence only
         const uint32_t lim = static_cast<uint32_t>(min(max(w.Lk - k0, 0), kBN)) * rsb;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc_uniform(
             static_cast<const char*>(a.k) + (w.k_base + static_cast<int64_t>(k0) * a.k_ss) * kEB,
             lim);
 #pragma unroll
@@ -492,7 +492,7 @@ struct TileLoader {
     if constexpr (BUF) {
       if constexpr (MODE == FA2_LAYOUT_PAGED) {
         const __amdgpu_buffer_rsrc_t rs =
-            make_rsrc(static_cast<const char*>(a.v) + w.v_base * kEB, a.pool_bytes_v);
+            make_rsrc_uniform(static_cast<const char*>(a.v) + w.v_base * kEB, a.pool_bytes_v);
 #pragma unroll
         for (int j = 0; j < kKPT; ++j) {
           const int n = k0 + vkey0 + j;
@@ -505,7 +505,7 @@ struct TileLoader {
         const uint32_t rsb = static_cast<uint32_t>(a.v_ss * kEB);
         // the descriptor covers this tile's rows inside the sequence only
         const uint32_t lim = static_cast<uint32_t>(min(max(w.Lk - k0, 0), kBN)) * rsb;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc_uniform(
             static_cast<const char*>(a.v) + (w.v_base + static_cast<int64_t>(k0) * a.v_ss) * kEB,
             lim);
 #pragma unroll
