@@ -161,7 +161,24 @@ typedef struct fa2_params {
    * the host.  No counterpart in the reference, whose decode kernels do not
    * synchronise waves. */
   int32_t decode_spin_cap;
+
+  /* fa2_fwd, fp16/bf16, head_dim 64 or 128: which forward kernel serves the
+   * call (enum fa2_kernel).  FA2_KERNEL_AUTO lets the library choose: calls
+   * whose regular grid fills at most half of the compute units and whose KV
+   * range is at most 32 tiles of 64 keys run the short-problem kernel (the KV
+   * tiles of each 32-row query block split over the waves of one workgroup,
+   * merged in LDS); FA2_KERNEL_REGULAR never uses it; FA2_KERNEL_SHORT uses it
+   * whenever dtype and head dim allow (num_splits 0 or 1, no max_workgroups).
+   * Results agree within rounding, not bit for bit.  No counterpart in the
+   * reference; tests use it to reach each kernel on small shapes. */
+  int32_t kernel;
 } fa2_params;
+
+enum fa2_kernel {
+  FA2_KERNEL_AUTO = 0,
+  FA2_KERNEL_REGULAR = 1,
+  FA2_KERNEL_SHORT = 2
+};
 
 /* Bytes of device workspace fa2_fwd needs for `p` (0 is possible).
  * Replaces the reference's per-call torch.empty of running_sum/max/acc

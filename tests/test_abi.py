@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layout_matches():
     assert _fa2.lib().fa2_params_size() == ctypes.sizeof(_fa2.Fa2Params)
-    assert _fa2.lib().fa2_abi_version() == _fa2.ABI_VERSION == 6
+    assert _fa2.lib().fa2_abi_version() == _fa2.ABI_VERSION == 7
 
 
 def test_strerror_for_every_code():
@@ -71,7 +71,7 @@ def rc_fwd(p):
     ("layout", 3, 2), ("dtype", 7, 3), ("mask", 5, 4), ("q_heads", 7, 5), ("batch", -1, 5),
     ("head_dim", 96, 6), ("q_ss", 100, 7), ("num_splits", 65, 11), ("num_splits", -1, 11),
     ("max_workgroups", -1, 5), ("kv_len_max", -1, 5), ("arith", 2, 3), ("arith", -1, 3),
-    ("decode_spin_cap", -1, 5),
+    ("decode_spin_cap", -1, 5), ("kernel", 3, 5), ("kernel", -1, 5),
     ("k_ss", (1 << 24) + 8, 13),  # a 32 MiB+ row stride: tile offsets leave 32 bits
 ])
 def test_validation_errors(field, value, code):

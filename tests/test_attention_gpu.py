@@ -40,9 +40,13 @@ def fa2():
 
 
 def run_case(case, layout, causal, alignment="top_left", shuffled=False, num_splits=0,
-             seed=0, page=16):
+             seed=0, page=16, kernel="regular"):
+    """One flash_attention_v2 call of `case`.  The tests of this module target
+    the regular kernels (two-head, one-head LDS, register-staged), so their
+    small shapes pin kernel="regular"; test_short_gpu.py runs the same cases
+    through the short-problem kernel."""
     q, k, v, kw = pack(case, layout, device=DEV, shuffled_pages=shuffled, seed=seed, page=page)
-    extra = {}
+    extra = {"kernel": kernel}
     if alignment != "top_left":
         extra["causal_alignment"] = alignment
     if num_splits:

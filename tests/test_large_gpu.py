@@ -63,15 +63,18 @@ def big_pool(seqs, page, min_bytes, seed):
     return cache, table.to(DEV)
 
 
-# (q heads, kv heads, dtype): the two-head kernel (even groups), the one-head
-# LDS kernel (odd groups) and the register-staged fp32 kernel
-KERNELS = [(8, 2, torch.bfloat16), (6, 2, torch.float16), (8, 2, torch.float32)]
+# (q heads, kv heads, dtype, kernel choice): the two-head kernel (even
+# groups), the one-head LDS kernel (odd groups), the register-staged fp32
+# kernel and the short-problem kernel
+KERNELS = [(8, 2, torch.bfloat16, "regular"), (6, 2, torch.float16, "regular"),
+           (8, 2, torch.float32, "regular"), (8, 2, torch.bfloat16, "short")]
+KERNEL_IDS = ["pp", "lds", "f32", "short"]
 
 
-@pytest.mark.parametrize("qh,kvh,dtype", KERNELS, ids=["pp", "lds", "f32"])
+@pytest.mark.parametrize("qh,kvh,dtype,kernel", KERNELS, ids=KERNEL_IDS)
 @pytest.mark.parametrize("page", [16, 5])
 @pytest.mark.parametrize("causal", [False, True])
-def test_paged_pool_over_2gib(qh, kvh, dtype, page, causal):
+def test_paged_pool_over_2gib(qh, kvh, dtype, kernel, page, causal):
     from kernels.attention import flash_attention_v2
     case = make_case(3, qh, kvh, 128, "self", dtype, "paged", 5000 + page + int(causal) + qh,
                      q_range=(50, 400))
@@ -81,7 +84,7 @@ def test_paged_pool_over_2gib(qh, kvh, dtype, page, causal):
     q = pack(case, "paged")[0].to(DEV)
     kw = dict(kv_indptr=torch.tensor(case.kv_lens, dtype=torch.int32, device=DEV),
               k_block_table=kt, v_block_table=vt, kv_page_size=page)
-    out = flash_attention_v2(q, kc, vc, is_causal=causal, **kw)
+    out = flash_attention_v2(q, kc, vc, is_causal=causal, kernel=kernel, **kw)
     torch.cuda.synchronize()
     check_all(case, "paged", causal, unpack(case, "paged", out.cpu(), kw))
     del kc, vc
@@ -144,7 +147,7 @@ def test_ragged_kv_over_2gib():
     torch.cuda.empty_cache()
 
 
-def unknown_pool_fwd(q, k, v, kw, causal, alignment="top_left", num_splits=0):
+def unknown_pool_fwd(q, k, v, kw, causal, alignment="top_left", num_splits=0, kernel="auto"):
     """flash_attention_v2's paged call with kv_len = 0 in fa2_params (the
     pool size unknown to the library; kv_len_max as the wrapper passes it,
     so that the split factor, and with it the arithmetic, is the same)."""
@@ -159,16 +162,18 @@ def unknown_pool_fwd(q, k, v, kw, causal, alignment="top_left", num_splits=0):
             o_strides=strides(out), kvi=index_tensor(kw["kv_indptr"], q.device),
             kt=table(kw["k_block_table"], q.device), vt=table(kw["v_block_table"], q.device),
             page_size=kw["kv_page_size"],
-            kv_len_max=kw["k_block_table"].shape[1] * kw["kv_page_size"])
+            kv_len_max=kw["k_block_table"].shape[1] * kw["kv_page_size"],
+            kernel={"auto": _fa2.KERNEL_AUTO, "regular": _fa2.KERNEL_REGULAR,
+                    "short": _fa2.KERNEL_SHORT}[kernel])
     return out
 
 
-@pytest.mark.parametrize("qh,kvh,dtype", KERNELS + [(8, 1, torch.float16)],
-                         ids=["pp", "lds", "f32", "mqa"])
+@pytest.mark.parametrize("qh,kvh,dtype,kernel", KERNELS + [(8, 1, torch.float16, "regular")],
+                         ids=KERNEL_IDS + ["mqa"])
 @pytest.mark.parametrize("page", [16, 8, 5, 1])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("splits", [0, 3])
-def test_paged_unknown_pool_size(qh, kvh, dtype, page, causal, splits):
+def test_paged_unknown_pool_size(qh, kvh, dtype, kernel, page, causal, splits):
     """kv_len = 0: the BUF = false kernels (per-page descriptors, or 64-bit
     row addresses for page sizes that are not a multiple of 4/8 rows), against
     the oracle and bitwise against the call with the pool size."""
@@ -176,8 +181,10 @@ def test_paged_unknown_pool_size(qh, kvh, dtype, page, causal, splits):
     case = make_case(3, qh, kvh, 64 if page == 8 else 128, "self", dtype, "paged",
                      5300 + page + 2 * int(causal) + qh, q_range=(1, 300))
     q, k, v, kw = pack(case, "paged", device=DEV, shuffled_pages=True, seed=page, page=page)
-    out = unknown_pool_fwd(q, k, v, kw, causal, num_splits=splits)
-    ref = flash_attention_v2(q, k, v, is_causal=causal, num_splits=splits, **kw)
+    if kernel == "short" and splits > 1:
+        pytest.skip("the short-problem kernel does not split across workgroups")
+    out = unknown_pool_fwd(q, k, v, kw, causal, num_splits=splits, kernel=kernel)
+    ref = flash_attention_v2(q, k, v, is_causal=causal, num_splits=splits, kernel=kernel, **kw)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu().view(torch.int16), ref.cpu().view(torch.int16))
     check_all(case, "paged", causal, unpack(case, "paged", out.cpu(), kw))

@@ -17,6 +17,7 @@
 #include "fa2_device.h"
 #include "fa2_kernel_lds.h"
 #include "fa2_kernel_pp.h"
+#include "fa2_kernel_short.h"
 #include "fa2_kernel_decode.h"
 #include "fa2_kernel_f32.h"
 #include "fa2_kv_append.h"
@@ -29,6 +30,10 @@
 // 1: the two-head kernel runs one workgroup per CU over all units
 #ifndef FA2_PP_PERSISTENT
 #define FA2_PP_PERSISTENT 1
+#endif
+// 1: calls too small to fill the GPU run the short-problem kernel (see make_plan)
+#ifndef FA2_SHORT
+#define FA2_SHORT 1
 #endif
 
 namespace fa2 {
@@ -73,6 +78,7 @@ struct Plan {
   int64_t npairs;   // work_ub * Hkv
   int64_t grid_x;   // npairs rounded up to kXcds, times Hq / Hkv
   bool pp;          // two-head ping-pong kernel
+  bool shortk;      // short-problem kernel: 32-row blocks, KV split over the waves
   bool qpair;       // ... on MHA, two q-blocks of one head per unit (KArgs::qpair)
   int64_t grid_pp;  // its grid: npairs rounded up to kXcds, times Hq / Hkv / 2
   int splits;
@@ -143,6 +149,7 @@ int validate(const fa2_params* p) {
   if (p->max_workgroups < 0 || p->kv_len_max < 0) return FA2_ERR_BAD_SHAPE;
   if (p->arith < FA2_ARITH_REFERENCE || p->arith > FA2_ARITH_FP32) return FA2_ERR_BAD_DTYPE;
   if (p->decode_spin_cap < 0) return FA2_ERR_BAD_SHAPE;
+  if (p->kernel < FA2_KERNEL_AUTO || p->kernel > FA2_KERNEL_SHORT) return FA2_ERR_BAD_SHAPE;
   return FA2_OK;
 }
 
@@ -182,6 +189,9 @@ int finish_plan(const fa2_params* p, Plan* pl);
 int64_t kv_upper_bound(const fa2_params* p) {
   int64_t ub = p->kv_len > 0 ? p->kv_len : INT32_MAX;
   if (p->kv_len_max > 0 && p->kv_len_max < ub) ub = p->kv_len_max;
+  // top-left causal: row i sees keys j <= i, so no sweep is longer than the
+  // query rows (dense/paged: the rows per sequence; ragged: all of them)
+  if (p->mask == FA2_MASK_CAUSAL_TOP_LEFT && p->q_len > 0 && p->q_len < ub) ub = p->q_len;
   return ub;
 }
 
@@ -203,7 +213,33 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   pl->pp = FA2_PP && p->dtype != FA2_DTYPE_F32 && group % 2 == 0 && fast_dim(p->head_dim);
   pl->grid_pp = cdiv(pl->npairs, kXcds) * kXcds * cdiv(group, 2);
 
-  int splits = p->num_splits;
+  // A call whose regular grid fills at most half of the CUs and whose KV
+  // range is short runs the short-problem kernel (fa2_kernel_short.h): four
+  // workgroups per 128-row q-block, each splitting its KV tiles over its 4
+  // waves and merging them in LDS, so the launch lasts about a quarter of
+  // the longest KV sweep instead of all of it, with no combine launch.
+  // Only with automatic splits and no grid cap (the persistent kernel's
+  // tests cap the grid).
+  pl->shortk = false;
+  if (p->kernel == FA2_KERNEL_SHORT && p->num_splits <= 1 && p->max_workgroups == 0 &&
+      p->dtype != FA2_DTYPE_F32 && fast_dim(p->head_dim)) {
+    pl->shortk = true;
+  } else if (FA2_SHORT && p->kernel == FA2_KERNEL_AUTO && p->num_splits == 0 &&
+             p->max_workgroups == 0 && p->dtype != FA2_DTYPE_F32 && fast_dim(p->head_dim)) {
+    // It pays only when its whole grid is resident at once (LDS: two
+    // workgroups per CU at head_dim 64, one at 128) and the regular
+    // kernel's KV sweeps are long enough for the split to matter.  Measured
+    // on MI355X (HIP-graph replays, GPU time): c1 (B1 H8 L512 D64 causal,
+    // 128 short workgroups) 15.5 -> 6.5 us; the reference benchmark's
+    // B16 x 8-head points need 512 short workgroups at D128 and run
+    // 9-12 us regular against 11-12 short.
+    const int64_t cus = query_device ? cu_count_current_device() : 256;
+    const int64_t resident = cus * (p->head_dim <= 64 ? 2 : 1);
+    const int64_t tiles = cdiv(kv_upper_bound(p), kBN);
+    if (pl->grid_x * kShSub <= resident && tiles >= kShMinTiles && tiles <= kShMaxTiles)
+      pl->shortk = true;
+  }
+  int splits = pl->shortk ? 1 : p->num_splits;
   if (splits == 0) {
     // Split the KV sweep only when the grid cannot fill the GPU (two
     // resident workgroups per CU) and every split keeps >= 16 KV tiles
@@ -236,7 +272,8 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
                             (p->layout == FA2_LAYOUT_RAGGED && p->batch > 0 &&
                              p->q_len >= 4 * kBM * p->batch);
   pl->qpair = FA2_PP && p->dtype != FA2_DTYPE_F32 && group == 1 && fast_dim(p->head_dim) &&
-              splits == 1 && many_qblocks;
+              splits == 1 && many_qblocks && !pl->shortk;
+  if (pl->shortk) pl->pp = false;
   if (pl->qpair) {
     pl->pp = true;
     // ragged keeps its bound (sum over sequences of their pairs <= nqb + batch)
@@ -299,6 +336,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds;
   if (pl->grid_x > INT32_MAX || pl->npairs > INT32_MAX) return FA2_ERR_TOO_LARGE;
   pl->pp = false;
+  pl->shortk = false;
   pl->qpair = false;
   pl->grid_pp = 0;
   int splits = p->num_splits;
@@ -379,7 +417,11 @@ int launch_typed(const KArgs& a, const Plan& pl, hipStream_t st) {
       // (the two-head kernel's three K/V slots do not fit LDS at D = 256)
       bool launched = false;
       if constexpr (D <= 128) {
-        if (pl.pp) {
+        if (pl.shortk) {
+          FA2_LAUNCH_BUF(fa2_fwd_short_kernel, dim3(static_cast<uint32_t>(pl.grid_x * kShSub)),
+                         dim3(kShThreads));
+          launched = true;
+        } else if (pl.pp) {
           // persistent: at most one workgroup per CU walks the units
           int64_t wgs = pl.grid_pp;
           if (pl.splits == 1 && FA2_PP_PERSISTENT) {
@@ -426,7 +468,7 @@ int launch_dim(int64_t d, int mode, const KArgs& a, const Plan& pl, hipStream_t 
 
 using namespace fa2;
 
-extern "C" int fa2_abi_version(void) { return 6; }
+extern "C" int fa2_abi_version(void) { return 7; }
 
 extern "C" size_t fa2_params_size(void) { return sizeof(fa2_params); }
 

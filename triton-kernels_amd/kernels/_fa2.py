@@ -18,9 +18,10 @@ LAYOUT_DENSE, LAYOUT_RAGGED, LAYOUT_PAGED = 0, 1, 2
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 MASK_NONE, MASK_TOP_LEFT, MASK_BOTTOM_RIGHT = 0, 1, 2
 ARITH_REFERENCE, ARITH_FP32 = 0, 1
+KERNEL_AUTO, KERNEL_REGULAR, KERNEL_SHORT = 0, 1, 2
 MAX_SPLITS = 64
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Every symbol include/fa2.h declares.
 EXPORTS = ("fa2_fwd_workspace_size", "fa2_fwd", "fa2_fwd_noalloc", "fa2_strerror",
@@ -66,6 +67,7 @@ class Fa2Params(ctypes.Structure):
         ("kv_len_max", ctypes.c_int64),
         ("arith", ctypes.c_int32),
         ("decode_spin_cap", ctypes.c_int32),
+        ("kernel", ctypes.c_int32),
     ]
 
 

@@ -87,7 +87,8 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
             q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
             q_strides, o_strides, qi=None, kvi=None, kt=None, vt=None,
             page_size=None, max_workgroups: int = 0, kv_len_max: int = 0,
-            noalloc: bool = False, arith: int = 0, decode_spin_cap: int = 0) -> None:
+            noalloc: bool = False, arith: int = 0, decode_spin_cap: int = 0,
+            kernel: int = 0) -> None:
     """Fill ``fa2_params`` and enqueue ``fa2_fwd`` (``decode=False``) or
     ``fa2_decode_fwd`` on torch's current stream of ``q``'s device.
 
@@ -97,7 +98,8 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
     upper bound of every sequence's KV length (0 = unknown) and
     ``max_workgroups`` the cap on the persistent grid (0 = none), ``arith`` the
     fa2_arith of fp32 tensors (``_fa2.ARITH_FP32``: fp32 throughout),
-    ``decode_spin_cap`` the decode kernel's wait bound (tests only).  ``noalloc``
+    ``decode_spin_cap`` the decode kernel's wait bound (tests only), ``kernel``
+    the fa2_kernel choice of the forward kernel (``_fa2.KERNEL_AUTO``...).  ``noalloc``
     enqueues ``fa2_fwd_noalloc`` instead (no workspace; prefill only).  Everything but
     the pointers depends only on the call signature, so that part of the
     parameter block (and its workspace size) is built once per signature.
@@ -106,7 +108,7 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
     key = (decode, layout, q.dtype, mask, int(num_splits), dev.index, batch, q_heads, kv_heads,
            head_dim, q_len, kv_len, tuple(q_strides), tuple(o_strides), k.stride(), v.stride(),
            None if kt is None else (kt.stride(0), vt.stride(0), int(page_size)),
-           int(max_workgroups), int(kv_len_max), int(arith), int(decode_spin_cap))
+           int(max_workgroups), int(kv_len_max), int(arith), int(decode_spin_cap), int(kernel))
     cached = _PLAN_CACHE.get(key)
     if cached is None:
         p = _fa2.Fa2Params()
@@ -132,6 +134,7 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
         p.kv_len_max = int(kv_len_max)
         p.arith = int(arith)
         p.decode_spin_cap = int(decode_spin_cap)
+        p.kernel = int(kernel)
         # validation needs the layout's pointers; they are overwritten per call
         _set_pointers(p, q, k, v, out, qi, kvi, kt, vt)
         with torch.cuda.device(dev):

@@ -26,6 +26,10 @@ call is unchanged):
 * ``num_splits`` - force the split-KV factor (0 = automatic);
 * ``max_workgroups`` - cap the persistent kernel's grid (0 = one workgroup
   per compute unit), e.g. to leave compute units to concurrent work;
+* ``kernel`` - ``"auto"`` (default), ``"regular"`` or ``"short"``: whether
+  a small call (fp16/bf16, head_dim 64/128) may run the short-problem kernel
+  that splits each 32-row query block's KV range over the waves of one
+  workgroup (``fa2_params.kernel``); results agree within rounding;
 * tensors whose last dimension is not contiguous or whose rows are not
   16-byte aligned are copied to a contiguous layout first (the reference
   silently assumes contiguity, attention.py:465-514).
@@ -53,16 +57,21 @@ def flash_attention_v2(
     causal_alignment: str = "top_left",
     num_splits: int = 0,
     max_workgroups: int = 0,
+    kernel: str = "auto",
 ) -> torch.Tensor:
     return _attention(q, k, v, is_causal=is_causal, q_indptr=q_indptr, kv_indptr=kv_indptr,
                       k_block_table=k_block_table, v_block_table=v_block_table,
                       kv_page_size=kv_page_size, causal_alignment=causal_alignment,
                       num_splits=num_splits, max_workgroups=max_workgroups,
-                      arith=_fa2.ARITH_REFERENCE)
+                      arith=_fa2.ARITH_REFERENCE, kernel=kernel)
+
+
+_KERNELS = {"auto": _fa2.KERNEL_AUTO, "regular": _fa2.KERNEL_REGULAR, "short": _fa2.KERNEL_SHORT}
 
 
 def _attention(q, k, v, *, is_causal, q_indptr, kv_indptr, k_block_table, v_block_table,
-               kv_page_size, causal_alignment, num_splits, max_workgroups, arith):
+               kv_page_size, causal_alignment, num_splits, max_workgroups, arith,
+               kernel="auto"):
     """The shared body of both entry points; ``arith`` is the fa2_arith of
     fp32 tensors (v2: the reference's fp16 rounding; v1: fp32)."""
     # --- assertion sequence of attention.py:762-834, in order -------------
@@ -137,6 +146,8 @@ def _attention(q, k, v, *, is_causal, q_indptr, kv_indptr, k_block_table, v_bloc
     check_dtype_and_dim("flash_attention_v2", q.dtype, head_dim)
     if causal_alignment not in ("top_left", "bottom_right"):
         raise ValueError("causal_alignment must be 'top_left' or 'bottom_right'")
+    if kernel not in _KERNELS:
+        raise ValueError("kernel must be 'auto', 'regular' or 'short'")
 
     q = prep(q)
     k = prep(k)
@@ -163,7 +174,8 @@ def _attention(q, k, v, *, is_causal, q_indptr, kv_indptr, k_block_table, v_bloc
             q=q, k=k, v=v, out=out, q_strides=strides(q), o_strides=strides(out),
             qi=qi, kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size,
             max_workgroups=max_workgroups,
-            kv_len_max=N if layout == _fa2.LAYOUT_PAGED else 0, arith=arith)
+            kv_len_max=N if layout == _fa2.LAYOUT_PAGED else 0, arith=arith,
+            kernel=_KERNELS[kernel])
     return out
 
 
