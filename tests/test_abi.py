@@ -236,3 +236,16 @@ def test_noalloc_rejects_before_any_launch():
     p = dense_params(num_splits=64, q=16, k=16, v=16, o=16)
     assert rc_ws(p)[1] > _fa2.NOALLOC_SCRATCH_BYTES
     assert lib.fa2_fwd_noalloc(ctypes.byref(p), None) == 15
+
+
+def test_launch_extension_loads_and_shares_the_library():
+    """The PyTorch-ROCm launch extension (csrc/fa2_torch.cpp) is built next to
+    libfa2.so, links it by soname, and the process maps one copy of it
+    whichever of ctypes and the extension loads it first."""
+    from kernels import _launch
+    x = _launch.ext()
+    assert x is not None, _launch._EXT_ERROR
+    assert callable(x.fwd)
+    _fa2.lib()
+    maps = [l for l in open("/proc/self/maps") if l.rstrip().endswith("libfa2.so")]
+    assert len({l.split()[-1] for l in maps}) == 1

@@ -57,6 +57,24 @@ def table(t: torch.Tensor, device) -> torch.Tensor:
     return t
 
 
+_EXT = None
+_EXT_ERROR = None
+
+
+def ext():
+    """The PyTorch-ROCm launch extension (csrc/fa2_torch.cpp, built in-tree by
+    build.py next to libfa2.so), or None when it is not built; its launch
+    calls the same libfa2.so entry point as the ctypes path below."""
+    global _EXT, _EXT_ERROR
+    if _EXT is None and _EXT_ERROR is None:
+        try:
+            from . import fa2_torch
+            _EXT = fa2_torch
+        except ImportError as e:  # not built: the ctypes path launches
+            _EXT_ERROR = e
+    return _EXT
+
+
 def check_dtype_and_dim(name: str, dtype, head_dim: int) -> None:
     """Checks of this build (the reference would fail inside Triton)."""
     if dtype not in DTYPES:

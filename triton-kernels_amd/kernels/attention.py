@@ -40,7 +40,13 @@ from __future__ import annotations
 import torch
 
 from . import _fa2
-from ._launch import check_dtype_and_dim, enqueue, index_tensor, prep, rows_ok, strides, table
+from ._launch import (check_dtype_and_dim, enqueue, ext, index_tensor, prep, rows_ok, strides,
+                      table)
+
+# The launch goes through the C++ extension (one call: sizes, alignment,
+# output, workspace, fa2_fwd) when it is built, else through ctypes; both
+# enqueue the same libfa2.so entry point with the same parameter block.
+USE_EXT = True
 
 
 def flash_attention_v2(
@@ -149,6 +155,17 @@ def _attention(q, k, v, *, is_causal, q_indptr, kv_indptr, k_block_table, v_bloc
     if kernel not in _KERNELS:
         raise ValueError("kernel must be 'auto', 'regular' or 'short'")
 
+    mask = (_fa2.MASK_NONE if not is_causal else
+            (_fa2.MASK_TOP_LEFT if causal_alignment == "top_left" else _fa2.MASK_BOTTOM_RIGHT))
+    x = ext() if USE_EXT else None
+    if x is not None:
+        return x.fwd(q, k, v, layout, mask, q_indptr if layout == _fa2.LAYOUT_RAGGED else None,
+                      kv_indptr if layout != _fa2.LAYOUT_DENSE else None,
+                      k_block_table if layout == _fa2.LAYOUT_PAGED else None,
+                      v_block_table if layout == _fa2.LAYOUT_PAGED else None,
+                      kv_page_size if layout == _fa2.LAYOUT_PAGED else 0, int(num_splits),
+                      int(max_workgroups), int(arith), _KERNELS[kernel])
+
     q = prep(q)
     k = prep(k)
     v = prep(v)
@@ -157,8 +174,6 @@ def _attention(q, k, v, *, is_causal, q_indptr, kv_indptr, k_block_table, v_bloc
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
     dev = q.device
-    mask = (_fa2.MASK_NONE if not is_causal else
-            (_fa2.MASK_TOP_LEFT if causal_alignment == "top_left" else _fa2.MASK_BOTTOM_RIGHT))
     qi = kvi = kt = vt = None
     if layout == _fa2.LAYOUT_RAGGED:
         qi = index_tensor(q_indptr, dev)
