@@ -29,7 +29,8 @@ constexpr int kShMaxTiles = 32;          // KV ranges (64-key tiles) the automat
 constexpr int kShMinTiles = 8;           // gives this kernel
 
 template <int DT, int D, int MODE, bool BUF>
-__global__ __launch_bounds__(kShThreads, 2) void fa2_fwd_short_kernel(KArgs a) {
+// (LDS: two workgroups per CU at D = 64, one at 128)
+__global__ __launch_bounds__(kShThreads, D > 64 ? 1 : 2) void fa2_fwd_short_kernel(KArgs a) {
   static_assert(DT != FA2_DTYPE_F32, "fp32 uses the register-staged kernel");
   constexpr bool BF = Elt<DT>::kBF;
   constexpr int DC = D / 16;  // MFMA k-steps of S (16 head dims each)
