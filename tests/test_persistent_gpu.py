@@ -8,7 +8,7 @@ and first K/V tiles during the current unit's last phases, and rotates its
 three LDS slots across units.  ``max_workgroups`` caps the grid, so small
 problems exercise all of that: 1 workgroup walks every unit, 3 and 5 give
 grids that are not a multiple of the 8 XCDs (plain reversal), 8 and 16 the
-blocked reversal.  The capped output must equal the uncapped output bit for
+blocked reversal (dense) or unit claims (ragged and paged).  The capped output must equal the uncapped output bit for
 bit (every unit computes the same arithmetic wherever it runs) and pass the
 reference tolerance and the strict bar against the C oracle.
 """
@@ -96,6 +96,83 @@ def test_capped_grid_bottom_right_paged():
     out, _ = run(case, "paged", True, max_workgroups=2, alignment="bottom_right", shuffled=True)
     assert torch.equal(out.view(torch.int16), base.view(torch.int16))
     check_all(case, "paged", True, unpack(case, "paged", out, kw), alignment="bottom_right")
+
+
+# Ragged and paged launches of >= 8 workgroups (one split) claim their
+# units: workgroup g takes unit g, then the next indices of counter g mod 8
+# (zeroed by the plan kernel), over a list that keeps each sequence's
+# q-blocks together.  Grids of 1, 3 and 5 workgroups walk the static rounds,
+# so these caps also compare the two walks bit for bit.
+CLAIM_CAPS = (1, 3, 8, 9, 13, 16, 40)
+MIXED_Q = [1, 40, 64, 65, 130, 300, 520, 700, 33, 257, 900, 128]
+MIXED_KV = [20, 64, 65, 1, 700, 300, 129, 64, 1000, 5, 256, 90]
+
+
+@pytest.mark.parametrize("layout", ["ragged", "paged"])
+@pytest.mark.parametrize("mask", ["none", "top_left", "bottom_right"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_claimed_units_mixed_lengths(layout, mask, dtype):
+    """One-tile units (claimed before the first barrier), units of two and
+    more tiles (claimed inside the tile loop), sequences shorter than a
+    q-block, and many claims per workgroup on the small caps."""
+    D = 128 if dtype == torch.bfloat16 else 64
+    seed = 4400 + 3 * ["none", "top_left", "bottom_right"].index(mask) + (layout == "paged")
+    causal = mask != "none"
+    kv = MIXED_Q if mask == "top_left" else MIXED_KV
+    # paged q is one padded length, which places the bottom-right diagonal
+    ql = [130] * len(MIXED_Q) if (layout, mask) == ("paged", "bottom_right") else MIXED_Q
+    case = make_case(len(MIXED_Q), 8, 2, D, "self" if mask == "top_left" else "cross", dtype,
+                     layout, seed, q_lens=ql, kv_lens=kv)
+    align = "bottom_right" if mask == "bottom_right" else "top_left"
+    print(f"claims {layout} {mask} {dtype} seed={seed}", flush=True)
+    base, kw = run(case, layout, causal, alignment=align, shuffled=layout == "paged")
+    for wgs in CLAIM_CAPS:
+        out, _ = run(case, layout, causal, max_workgroups=wgs, alignment=align,
+                     shuffled=layout == "paged")
+        assert torch.equal(out.view(torch.int16), base.view(torch.int16)), wgs
+    check_all(case, layout, causal, unpack(case, layout, base, kw), alignment=align)
+
+
+@pytest.mark.parametrize("layout", ["ragged", "paged"])
+def test_claimed_units_empty_kv(layout):
+    """Sequences with no keys give units of no tiles, which claim through a
+    barrier of their own: their rows are NaN (0/0, as the reference), and
+    every other sequence's rows equal, bit for bit, a call without them."""
+    from kernels.attention import flash_attention_v2
+    ql = [200, 64, 300, 129, 90, 260, 40, 500]
+    kl = [300, 1, 700, 65, 1, 128, 64, 900]
+    empty = [1, 4]
+    case = make_case(len(ql), 8, 2, 128, "cross", torch.bfloat16, layout, 4500, q_lens=ql,
+                     kv_lens=kl)
+    keep = [b for b in range(len(ql)) if b not in empty]
+    sub = make_case(len(keep), 8, 2, 128, "cross", torch.bfloat16, layout, 4500,
+                    q_lens=[ql[b] for b in keep], kv_lens=[kl[b] for b in keep])
+    sub.qs[:] = [case.qs[b] for b in keep]
+    sub.ks[:] = [case.ks[b] for b in keep]
+    sub.vs[:] = [case.vs[b] for b in keep]
+    print(f"claims empty kv {layout}", flush=True)
+    ref, rkw = run(sub, layout, False)
+    ref = unpack(sub, layout, ref, rkw)
+    for wgs in (0, 8, 11):
+        q, k, v, kw = pack(case, layout, device=DEV)
+        if layout == "ragged":
+            ip = [0]
+            for b in range(len(kl)):
+                ip.append(ip[-1] + (0 if b in empty else kl[b]))
+            k = torch.cat([case.ks[b] for b in range(len(kl)) if b not in empty]).to(DEV)
+            v = torch.cat([case.vs[b] for b in range(len(kl)) if b not in empty]).to(DEV)
+            kw["kv_indptr"] = torch.tensor(ip, dtype=torch.int32, device=DEV)
+        else:
+            lens = torch.tensor(kl, dtype=torch.int32)
+            lens[empty] = 0
+            kw["kv_indptr"] = lens.to(DEV)
+        out = flash_attention_v2(q, k, v, is_causal=False, max_workgroups=wgs,
+                                 kernel="regular", **kw).cpu()
+        outs = unpack(case, layout, out, kw)
+        for b in empty:
+            assert torch.isnan(outs[b].float()).all(), (wgs, b)
+        for i, b in enumerate(keep):
+            assert torch.equal(outs[b].view(torch.int16), ref[i].view(torch.int16)), (wgs, b)
 
 
 def test_max_workgroups_only_caps():

@@ -120,6 +120,12 @@ struct KArgs {
   // KV tiles of block 2k + 1 (the extra tiles are fully masked for block 2k
   // under a causal mask and add exact zeros); nqb then counts pairs.
   int32_t qpair;
+  // Two-head kernel with a plan and one split: kXcds unit counters, zeroed
+  // by the plan kernel.  Workgroup g takes unit g first and then claims the
+  // next units of its group (g mod kXcds) from counter g mod kXcds; the plan
+  // lists each sequence's q-blocks together (sequence-major).  null: the
+  // static round walk over a heaviest-first list.
+  int32_t* claim;
 };
 
 // ---------------------------------------------------------------------------
@@ -963,13 +969,26 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     if (tid == 0) *work_count = a.batch < a.work_ub ? a.batch : a.work_ub;
     return;
   }
+  // Sequence-major list (claimed units): every sequence's items form one
+  // run, heaviest first, and the runs are ordered by their heaviest item,
+  // so the workgroups that claim consecutive units of a group share one
+  // sequence's K/V in their L2.  An item's cost never decreases with its
+  // q-block under any mask, so item j of n sits at n - 1 - j in its run.
+  const bool seq_major = a.claim != nullptr;
+  if (seq_major && tid < kXcds) a.claim[tid] = 0;
   for (int i = tid; i < kCostBuckets; i += kPlanThreads) hist[i] = 0;
   __syncthreads();
   for (int b = tid; b < a.batch; b += kPlanThreads) {
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + a.block_rows - 1) / a.block_rows;
-    for (int j = 0; j < plan_items(a, nq); ++j)
+    const int ni = plan_items(a, nq);
+    if (seq_major) {
+      if (ni > 0)
+        atomicAdd(&hist[block_cost(a.mask, plan_cost_block(a, ni - 1, nq), Lq, Lk, false)], ni);
+      continue;
+    }
+    for (int j = 0; j < ni; ++j)
       atomicAdd(&hist[block_cost(a.mask, plan_cost_block(a, j, nq), Lq, Lk, a.pack_m > 0)], 1);
   }
   __syncthreads();
@@ -1004,7 +1023,19 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + a.block_rows - 1) / a.block_rows;
-    for (int j = 0; j < plan_items(a, nq); ++j) {
+    const int ni = plan_items(a, nq);
+    if (seq_major) {
+      if (ni > 0) {
+        const int pos0 = atomicAdd(
+            &hist[block_cost(a.mask, plan_cost_block(a, ni - 1, nq), Lq, Lk, false)], ni);
+        for (int j = 0; j < ni; ++j) {
+          const int pos = pos0 + ni - 1 - j;
+          if (pos < a.work_ub) work[pos] = make_int2(b, j);
+        }
+      }
+      continue;
+    }
+    for (int j = 0; j < ni; ++j) {
       const int pos =
           atomicAdd(&hist[block_cost(a.mask, plan_cost_block(a, j, nq), Lq, Lk, a.pack_m > 0)], 1);
       if (pos < a.work_ub) work[pos] = make_int2(b, j);

@@ -116,7 +116,9 @@ struct PPUnit {
   bool hok;                // this group's head exists (odd head groups)
 };
 
-template <int DT, int D, int MODE, bool BUF>
+// CLAIM: the unit walk by claims (KArgs::claim, ragged/paged only), a
+// separate instantiation so that the static walk keeps its registers.
+template <int DT, int D, int MODE, bool BUF, bool CLAIM = false>
 __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   static_assert(DT != FA2_DTYPE_F32, "fp32 uses the register-staged kernel");
   constexpr bool BF = Elt<DT>::kBF;
@@ -195,8 +197,21 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
     u.T = (ntiles * (split + 1)) / S - u.t_begin;
     return true;
   };
+  // Claimed units (a.claim): workgroup g walks units L = c * kXcds + g mod
+  // kXcds of its group, c = g / kXcds first, then the indices its group's
+  // counter hands out; r is then c.  Units of a group are valid up to some
+  // index and invalid after it (the work list's order), so the first invalid
+  // one ends the walk.
+  static_assert(!CLAIM || MODE != FA2_LAYOUT_DENSE, "claims need the plan kernel's counters");
+  constexpr bool dyn = CLAIM;
+  const int xg = blockIdx.x % kXcds;
+  const int n_x = (P - xg + kXcds - 1) / kXcds;  // workgroups of the group
   // next valid unit at round >= r (uniform); false when none is left
   auto next_unit = [&](int& r, PPUnit& u) -> bool {
+    if (dyn) {
+      const int L = r * kXcds + xg;
+      return L >= 0 && L < a.units && make_unit(L, u);
+    }
     for (;; ++r) {
       const int L = unit_index(r);
       if (L >= a.units) return false;
@@ -246,7 +261,38 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   using Y = std::integral_constant<bool, true>;
   using N = std::integral_constant<bool, false>;
 
-  int r = 0;
+  // Claims: wave 0 adds 1 to its group's counter (one lane, returning the
+  // old value) a few tiles before its unit ends; the atomic is issued before
+  // that phase's tile loads, so the phase's wait for them (vmcnt counts
+  // complete in issue order) also covers it.  The claimed index goes to the
+  // other waves through LDS across the phase barrier, in one of two words
+  // by claim parity: a word is written again only after every wave has
+  // passed the barrier that publishes the claim in between, after its read.
+  __shared__ int claim_next[2];
+  int nclaim = 0;
+  uint32_t claimed = 0;
+  auto claim_issue = [&]() {
+    if (lane == 0)
+      asm volatile("global_atomic_add %0, %1, %2, off sc0"
+                   : "=v"(claimed)
+                   : "v"(a.claim + xg), "v"(1u)
+                   : "memory");
+  };
+  // after a wait that covers the atomic (vmcnt); before a pp_barrier()
+  auto claim_publish = [&]() {
+    asm volatile("" : "+v"(claimed));  // no use of the value before the wait
+    const int c = __builtin_amdgcn_readfirstlane(claimed);
+    if (lane == 0) claim_next[nclaim & 1] = n_x + c;
+  };
+  // after that barrier (all waves)
+  auto claim_read = [&]() -> int {
+    const int c = *static_cast<volatile int*>(&claim_next[nclaim & 1]);
+    ++nclaim;
+    return __builtin_amdgcn_readfirstlane(c);
+  };
+  constexpr int kClaimLead = 2;  // tiles between the claim and the unit's last tile
+
+  int r = dyn ? static_cast<int>(blockIdx.x) / kXcds : 0;
   PPUnit cur;
   if (!next_unit(r, cur)) return;
   int gb = 0;          // tile i of the current unit is tile gb + i of this workgroup's stream
@@ -446,12 +492,20 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       ld.template issue<true>(a, v.w, v.t_begin * kBN, v0s);
     };
 
+    // tile of the claim (T >= 2); a one-tile unit claims before its first barrier
+    const int i_claim = T - 1 - kClaimLead > 0 ? T - 1 - kClaimLead : 0;
     if (T > 0) {
       if (grp == 0) {
+        const bool claim_now = dyn && T == 1 && wave == 0;
+        if (claim_now) claim_issue();
         if (!pre) issue_first(u, gb);
         // K(0) (and Q) have landed: what was issued after K(0) may be in
         // flight (K(1), V(0), and the previous unit's output stores)
         wait_vm((T > 1 ? 2 * kI : kI) + (pre ? kStores : 0));
+        if (claim_now) {
+          pp_wait_vm<0>();
+          claim_publish();
+        }
       }
       pp_barrier();
       if (grp != 0) {
@@ -466,16 +520,21 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       pp_barrier();
       for (int i = 0; i + 1 < T; ++i) {
         int n = 0;
+        const bool claim_now = dyn && i == i_claim && wave == 0;
+        if (claim_now) claim_issue();
         if (grp == 0) n = issue_iter(i);
         phase_v(i);
         // K(i+1) and V(i) (read from M(i+1) on) have landed; the loads of
-        // the current issue may still be in flight
+        // the current issue may still be in flight (n >= kI: the claim,
+        // issued before them, has returned)
         if (grp == 0) wait_vm(n);
+        if (claim_now) claim_publish();
         pp_softmax_order();
         pp_barrier();
         phase_m(Y{}, Y{}, i + 1);
         pp_barrier();
       }
+      if (dyn) rn = claim_read();
       has_next = next_unit(rn, nxt);
       pre_next = has_next && nxt.T > 0 && S == 1;
       // Q of the next unit: this group's last S is done
@@ -499,6 +558,16 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       phase_m(Y{}, N{}, T);
       if (grp == 0) pp_barrier();  // pairs with group 1's last barrier
     } else {
+      if (dyn) {
+        // both groups have passed the same number of barriers here
+        if (wave == 0) {
+          claim_issue();
+          pp_wait_vm<0>();
+          claim_publish();
+        }
+        pp_barrier();
+        rn = claim_read();
+      }
       has_next = next_unit(rn, nxt);
     }
 
