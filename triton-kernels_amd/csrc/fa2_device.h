@@ -28,8 +28,9 @@
 //   * causal: tiles past the diagonal are never loaded, masks are evaluated
 //     only on diagonal / sequence-end tiles;
 //   * dense causal launches the heaviest q-blocks first; ragged and paged
-//     launches read a heaviest-first work list built on the device by
-//     fa2_plan_kernel (no host synchronisation, unlike attention.py:847).
+//     launches read a work list built on the device by fa2_plan_kernel (no
+//     host synchronisation, unlike attention.py:847): heaviest first, or
+//     sequence-major when the two-head kernel claims its units.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -97,7 +98,7 @@ struct KArgs {
   float scale_log2;     // softmax_scale * log2(e)
   uint32_t pool_bytes_k;  // paged + buffer path: bytes of the k cache from the kv-head 0 row 0
   uint32_t pool_bytes_v;
-  const int2* work;     // ragged/paged work list (b, q-block), heaviest first; null: no plan
+  const int2* work;     // ragged/paged work list (b, q-block) from the plan kernel; null: no plan
   const int32_t* work_count;
   float* part_ml;       // split partials: (m, l) per row
   float* part_o;        // split partials: unnormalised O per row
