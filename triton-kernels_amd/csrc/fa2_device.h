@@ -127,7 +127,20 @@ struct KArgs {
   // lists each sequence's q-blocks together (sequence-major).  null: the
   // static round walk over a heaviest-first list.
   int32_t* claim;
+  // Ragged/paged launches with automatic splits: the split count the plan
+  // kernel derives from the longest KV sweep (<= num_splits, the host's
+  // bound from the total KV rows), which the forward and combine kernels
+  // use instead of num_splits.  null: num_splits.
+  int32_t* split_count;
 };
+
+// Fewest KV tiles a split keeps (the automatic split heuristic).
+constexpr int kMinSplitTiles = 16;
+
+// The launch's split count: blockIdx.y >= it has no work.
+__device__ __forceinline__ int launch_splits(const KArgs& a) {
+  return a.split_count ? __builtin_amdgcn_readfirstlane(*a.split_count) : a.num_splits;
+}
 
 // ---------------------------------------------------------------------------
 // Element types.
@@ -612,7 +625,8 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : 2) void fa2_fwd_kernel(KArg
   if (!w.valid) return;
   const int q0 = w.qblk * kBM;
   const int split = blockIdx.y;
-  const int S = a.num_splits;
+  const int S = launch_splits(a);
+  if (split >= S) return;
 
   // KV tile range of this split.
   const int kv_end = kv_end_for_unit(a, q0, w.Lq, w.Lk, w.off);
@@ -849,6 +863,8 @@ constexpr int kCombineRows = kThreads / (D / 4);  // rows per workgroup
 
 template <int DT, int D, int MODE>
 __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
+  const int S = launch_splits(a);
+  if (S <= 1) return;  // the forward kernel wrote the output
   const Work w = decode_work<MODE>(a, blockIdx.x);
   if (!w.valid) return;
   constexpr int kTPR = D / 4;  // threads per row, 4 floats each
@@ -856,7 +872,6 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   const int col = (threadIdx.x % kTPR) * 4;
   const int qrow = w.qblk * a.block_rows + r;
   if (r >= a.part_rows || qrow >= w.Lq || col >= a.dv) return;
-  const int S = a.num_splits;
   const int64_t G = a.part_slots;
   const int64_t R = a.part_rows;
   const float* ml = a.part_ml + (static_cast<int64_t>(blockIdx.x) * R + r) * 2;
@@ -977,6 +992,8 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
   // q-block under any mask, so item j of n sits at n - 1 - j in its run.
   const bool seq_major = a.claim != nullptr;
   if (seq_major && tid < kXcds) a.claim[tid] = 0;
+  __shared__ int max_cost;  // KV tiles of the heaviest item
+  if (tid == 0) max_cost = 0;
   for (int i = tid; i < kCostBuckets; i += kPlanThreads) hist[i] = 0;
   __syncthreads();
   for (int b = tid; b < a.batch; b += kPlanThreads) {
@@ -984,6 +1001,9 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + a.block_rows - 1) / a.block_rows;
     const int ni = plan_items(a, nq);
+    if (ni > 0 && a.split_count)
+      atomicMax(&max_cost,
+                block_cost(a.mask, plan_cost_block(a, ni - 1, nq), Lq, Lk, a.pack_m > 0));
     if (seq_major) {
       if (ni > 0)
         atomicAdd(&hist[block_cost(a.mask, plan_cost_block(a, ni - 1, nq), Lq, Lk, false)], ni);
@@ -993,6 +1013,11 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
       atomicAdd(&hist[block_cost(a.mask, plan_cost_block(a, j, nq), Lq, Lk, a.pack_m > 0)], 1);
   }
   __syncthreads();
+  // the host's heuristic with the longest sweep in place of its bound
+  if (tid == 0 && a.split_count) {
+    const int s = max_cost / kMinSplitTiles;
+    *a.split_count = s < 1 ? 1 : (s < a.num_splits ? s : a.num_splits);
+  }
   // Exclusive scan in descending cost order: bucket c starts after all
   // buckets c' > c.  Thread t owns buckets [(P-1-t)*4, +4) from the top.
   constexpr int kPer = kCostBuckets / kPlanThreads;

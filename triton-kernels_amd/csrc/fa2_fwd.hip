@@ -98,6 +98,7 @@ struct Plan {
   bool dec;         // packed fp16/bf16: the decode kernel
   bool f32;         // fp32 arithmetic: the fp32-MFMA kernel
   bool plan;        // ragged/paged: the plan kernel orders the work list
+  bool dev_splits;  // ... and lowers the automatic split count (KArgs::split_count)
   bool buf;         // paged: every row of the pool has a 31-bit byte offset
   int64_t max_wgs;  // cap on the persistent grid (0: none)
   uint32_t pool_bytes_k, pool_bytes_v;
@@ -264,7 +265,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
     const int64_t units = pl->npairs * (p->q_heads / p->kv_heads);  // real workgroups
     if (units > 0 && units < slots) {
       int64_t s = cdiv(slots, units);
-      const int64_t by_tiles = tiles / 16;
+      const int64_t by_tiles = tiles / kMinSplitTiles;
       if (s > by_tiles) s = by_tiles;
       if (s > FA2_MAX_SPLITS) s = FA2_MAX_SPLITS;
       if (s < 1) s = 1;
@@ -296,6 +297,15 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   pl->dec = false;
   pl->f32 = p->dtype == FA2_DTYPE_F32 && p->arith == FA2_ARITH_FP32;
   pl->plan = p->layout != FA2_LAYOUT_DENSE;
+  // The split count above rests on the longest KV sweep any sequence can
+  // have; for ragged K/V that is the total of all sequences (the lengths
+  // stay on the device).  The plan kernel knows the longest sweep and lowers
+  // the count: a launch then runs the splits it needs out of a grid sized
+  // for the bound (the others exit at once), and with one the combine
+  // kernel exits at once.  Measured on MI355X (B16 Hq8/Hkv2 q128 kv128
+  // ragged, bf16 D128): 2 splits of 1 tile each, forward 14.1 us + combine
+  // 6.0 us.
+  pl->dev_splits = pl->plan && p->num_splits == 0 && splits > 1;
   pl->part_rows = kBM;  // the two-head kernel's partial slots assume kBM
   return finish_plan(p, pl);
 }
@@ -311,7 +321,7 @@ int finish_plan(const fa2_params* p, Plan* pl) {
   pl->off_work = off;
   if (p->layout != FA2_LAYOUT_DENSE) off += static_cast<size_t>(pl->work_ub) * sizeof(int2);
   off = (off + 255) & ~size_t(255);
-  pl->off_count = off;  // the item count, then the claim counters at kClaimOffset
+  pl->off_count = off;  // the item count, the split count, the claim counters at kClaimOffset
   if (p->layout != FA2_LAYOUT_DENSE) off += 256;
   pl->off_ml = off;
   if (splits > 1)
@@ -372,6 +382,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   // when the decode kernel's grid (one workgroup per CU) runs in more than
   // one round.  (d1: the 4.8 us plan launch was 7 % of the step.)
   pl->plan = p->layout != FA2_LAYOUT_DENSE;
+  pl->dev_splits = false;
   if (pl->plan && pl->dec && query_device &&
       pl->grid_x * splits <= cu_count_current_device())
     pl->plan = false;
@@ -608,6 +619,7 @@ int run(const fa2_params* p, void* stream, bool packed) {
   char* ws = static_cast<char*>(p->workspace);
   a.work = pl.plan ? reinterpret_cast<const int2*>(ws + pl.off_work) : nullptr;
   a.work_count = pl.plan ? reinterpret_cast<const int32_t*>(ws + pl.off_count) : nullptr;
+  a.split_count = pl.dev_splits ? reinterpret_cast<int32_t*>(ws + pl.off_count) + 1 : nullptr;
   a.part_ml = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
   a.part_o = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
   a.part_rows = pl.part_rows;

@@ -60,7 +60,8 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : 2) void fa2_fwd_f32_kernel(
   if (!w.valid) return;
   const int q0 = w.qblk * kBM;
   const int split = blockIdx.y;
-  const int S = a.num_splits;
+  const int S = launch_splits(a);
+  if (split >= S) return;
   const int kv_end = kv_end_for_unit(a, q0, w.Lq, w.Lk, w.off);
   const int ntiles = (kv_end + kBN - 1) / kBN;
   const int t_begin = (ntiles * split) / S;

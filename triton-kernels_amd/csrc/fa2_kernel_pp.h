@@ -147,7 +147,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   const int hi = lane >> 5;
   const int group = a.hq / a.hkv;
   const int split = blockIdx.y;
-  const int S = a.num_splits;
+  const int S = launch_splits(a);
+  if (split >= S) return;
   const bool causal = a.mask != FA2_MASK_NONE;
   char* const stage = lds + kSlotBytes + wave * OStage<kStageDims>::kBytes;
 
