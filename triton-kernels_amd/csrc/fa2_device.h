@@ -996,9 +996,14 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
   if (tid == 0) max_cost = 0;
   for (int i = tid; i < kCostBuckets; i += kPlanThreads) hist[i] = 0;
   __syncthreads();
+  int lq0 = 0, lk0 = 0;  // this thread's first sequence, kept for the second pass
   for (int b = tid; b < a.batch; b += kPlanThreads) {
     int Lq, Lk;
     seq_lens<MODE>(a, b, Lq, Lk);
+    if (b == tid) {
+      lq0 = Lq;
+      lk0 = Lk;
+    }
     const int nq = (Lq + a.block_rows - 1) / a.block_rows;
     const int ni = plan_items(a, nq);
     if (ni > 0 && a.split_count)
@@ -1020,7 +1025,11 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
   }
   // Exclusive scan in descending cost order: bucket c starts after all
   // buckets c' > c.  Thread t owns buckets [(P-1-t)*4, +4) from the top.
+  // A scan inside each wave (lane shuffles), then over the wave totals:
+  // two barriers.
   constexpr int kPer = kCostBuckets / kPlanThreads;
+  constexpr int kPlanWaves = kPlanThreads / 64;
+  __shared__ int wave_total[kPlanWaves];
   int local[kPer];
   int sum = 0;
 #pragma unroll
@@ -1028,17 +1037,27 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
     local[i] = hist[kCostBuckets - 1 - (tid * kPer + i)];
     sum += local[i];
   }
-  scan[tid] = sum;
-  __syncthreads();
-  for (int step = 1; step < kPlanThreads; step <<= 1) {
-    const int v = (tid >= step) ? scan[tid - step] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
+  const int lane = tid & 63, wv = tid >> 6;
+  int incl = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d);
+    if (lane >= d) incl += y;
   }
-  int run = scan[tid] - sum;
-  const int total = scan[kPlanThreads - 1];
+  if (lane == 63) wave_total[wv] = incl;
   __syncthreads();
+  if (wv == 0) {
+    int t = lane < kPlanWaves ? wave_total[lane] : 0;
+#pragma unroll
+    for (int d = 1; d < kPlanWaves; d <<= 1) {
+      const int y = __shfl_up(t, d);
+      if (lane >= d) t += y;
+    }
+    if (lane < kPlanWaves) wave_total[lane] = t;  // inclusive
+  }
+  __syncthreads();
+  int run = incl - sum + (wv > 0 ? wave_total[wv - 1] : 0);
+  const int total = wave_total[kPlanWaves - 1];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     hist[kCostBuckets - 1 - (tid * kPer + i)] = run;  // becomes the cursor
@@ -1046,8 +1065,8 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
   }
   __syncthreads();
   for (int b = tid; b < a.batch; b += kPlanThreads) {
-    int Lq, Lk;
-    seq_lens<MODE>(a, b, Lq, Lk);
+    int Lq = lq0, Lk = lk0;
+    if (b != tid) seq_lens<MODE>(a, b, Lq, Lk);
     const int nq = (Lq + a.block_rows - 1) / a.block_rows;
     const int ni = plan_items(a, nq);
     if (seq_major) {
