@@ -44,6 +44,11 @@
 namespace fa2 {
 namespace {
 
+// fp32 decode (the fp32-MFMA kernel in packed-head mode): automatic splits
+// aim at this many workgroups per CU, keeping this many KV tiles per split
+constexpr int64_t kF32DecodeWgsPerCu = 8;
+constexpr int64_t kF32DecodeMinTiles = 32;
+
 // byte offset of the kXcds claim counters after the work list's item count
 // (within the 256 bytes reserved there; a cache line of their own)
 constexpr size_t kClaimOffset = 128;
@@ -306,6 +311,17 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   // ragged, bf16 D128): 2 splits of 1 tile each, forward 14.1 us + combine
   // 6.0 us.
   pl->dev_splits = pl->plan && p->num_splits == 0 && splits > 1;
+  // A paged launch whose workgroups all fit on the GPU at once needs no
+  // list: every sequence has the same q-block count, so decode_work maps
+  // workgroups to items directly, and with every workgroup resident their
+  // order does not matter.  Measured on MI355X (B16 Hq8/Hkv2 q128 kv128
+  // paged, bf16 D128): the plan launch was 4.0 us of a 15.1 us call.
+  if (p->layout == FA2_LAYOUT_PAGED && !pl->dev_splits) {
+    const int64_t cus = query_device ? cu_count_current_device() : 256;
+    const int64_t per_split =
+        pl->shortk ? pl->grid_x * kShSub : (pl->pp ? pl->grid_pp : pl->grid_x);
+    if (per_split * splits <= cus) pl->plan = false;
+  }
   pl->part_rows = kBM;  // the two-head kernel's partial slots assume kBM
   return finish_plan(p, pl);
 }
@@ -361,14 +377,22 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   int splits = p->num_splits;
   if (splits == 0) {
     const int64_t cus = query_device ? cu_count_current_device() : 256;
-    // the decode kernel holds a CU alone: one workgroup per CU (measured on
-    // MI355X: 128 units of 128 tiles run best at 2 splits, 512 units at 1)
-    const int64_t target = cus;
+    // The decode kernel holds a CU alone: one workgroup per CU, >= 8 tiles
+    // per split to keep its LDS ring in steady state (measured on MI355X:
+    // 128 units of 128 tiles run best at 2 splits, 512 units at 1).  The
+    // fp32 kernel (two workgroups per CU, no deep K/V pipeline) is
+    // latency-bound: it wants several rounds of workgroups, each sweeping
+    // >= 32 tiles (measured on MI355X, fp32 decode, us per call at 1 / 2 /
+    // 4 / 8 workgroups per CU and >= 8 tiles: d1 (128 units of 128 tiles)
+    // 338 / 180 / 187 / 204 at 2 / 4 / 8 / 16 splits; d2 (512 units, up to
+    // 128 tiles) 1730 / 1731 / 1148 / 1105 at 1 / 1 / 2 / 4 splits).
+    const int64_t target = pl->dec ? cus : cus * kF32DecodeWgsPerCu;
+    const int64_t min_tiles = pl->dec ? 8 : kF32DecodeMinTiles;
     const int64_t tiles = cdiv(kv_upper_bound(p), kBN);
     splits = 1;
     if (pl->npairs > 0 && pl->npairs < target) {
       int64_t sp = cdiv(target, pl->npairs);
-      const int64_t by_tiles = tiles / 8;  // keep the LDS ring in steady state
+      const int64_t by_tiles = tiles / min_tiles;
       if (sp > by_tiles) sp = by_tiles;
       if (sp > FA2_MAX_SPLITS) sp = FA2_MAX_SPLITS;
       if (sp < 1) sp = 1;
@@ -379,12 +403,13 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   pl->part_rows = static_cast<int>(pl->rows < pl->block_rows ? pl->rows : pl->block_rows);
   // Every sequence has the same q-block count here, so decode_work can map
   // workgroups to items without a list; the heaviest-first order only pays
-  // when the decode kernel's grid (one workgroup per CU) runs in more than
-  // one round.  (d1: the 4.8 us plan launch was 7 % of the step.)
+  // when the grid runs in more than one round (the decode kernel: one
+  // workgroup per CU; the fp32 kernel: two).  (d1: the 4.8 us plan launch
+  // was 7 % of the step.)
   pl->plan = p->layout != FA2_LAYOUT_DENSE;
   pl->dev_splits = false;
-  if (pl->plan && pl->dec && query_device &&
-      pl->grid_x * splits <= cu_count_current_device())
+  if (pl->plan && (pl->dec || pl->f32) && query_device &&
+      pl->grid_x * splits <= cu_count_current_device() * (pl->dec ? 1 : 2))
     pl->plan = false;
   return finish_plan(p, pl);
 }
