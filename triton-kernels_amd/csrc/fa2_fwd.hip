@@ -675,9 +675,10 @@ extern "C" int fa2_fwd(const fa2_params* p, void* stream) { return run(p, stream
 // the process ends.  In host code the array's name is only a stand-in for the
 // symbol: its device address comes from hipGetSymbolAddress, once per device
 // with that device current, and only that address reaches the kernels.
-// Nothing in it has to start at zero: the plan kernel writes the work list
-// and its count, and every split partial the combine reads is written by the
-// forward kernel of the same call.
+// Nothing in it has to start at zero: the plan kernel writes the work list,
+// its count, the split count and zeroes the claim counters, and every split
+// partial the combine reads is written by the forward kernel of the same
+// call.
 static __device__ __align__(256) unsigned char scratch[FA2_NOALLOC_SCRATCH_BYTES];
 
 namespace fa2 {
