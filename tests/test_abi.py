@@ -115,6 +115,22 @@ def test_workspace_sizes():
     assert rc_ws(dense_params(batch=0)) == (0, 0)
 
 
+def test_fp32_workspace_holds_fp16_copies():
+    """fp32 tensors with the reference's fp16 rounding (flash_attention_v2)
+    at head_dim 64/128, dense or ragged: fp16 copies of q, k and v plus one
+    split's fp32 partials.  fp32 arithmetic (v1), other head dims and paged
+    pools need neither."""
+    q_el, kv_el = 2 * 8 * 300 * 128, 2 * 2 * 300 * 128
+    parts = 1 * (3 * 2 * 8) * 128 * (2 + 128) * 4  # 24 one-head units of 128 rows
+    rc, n = rc_ws(dense_params(dtype=2))
+    assert rc == 0 and n >= 2 * (q_el + 2 * kv_el) + parts
+    assert rc_ws(dense_params(dtype=2, arith=1)) == (0, 0)
+    rc, n = rc_ws(dense_params(dtype=2, head_dim=32, q_sh=300 * 32, q_ss=32, q_sb=8 * 300 * 32,
+                               k_sb=2 * 300 * 32, k_sh=300 * 32, k_ss=32, v_sb=2 * 300 * 32,
+                               v_sh=300 * 32, v_ss=32, o_sb=8 * 300 * 32, o_sh=300 * 32, o_ss=32))
+    assert (rc, n) == (0, 0)
+
+
 def test_workspace_too_small_is_rejected():
     p = dense_params(num_splits=2, q=16, k=16, v=16, o=16)
     rc, n = rc_ws(p)

@@ -132,6 +132,10 @@ struct KArgs {
   // bound from the total KV rows), which the forward and combine kernels
   // use instead of num_splits.  null: num_splits.
   int32_t* split_count;
+  // fp32 tensors on the 16-bit kernels (q/k/v are fp16 copies): the forward
+  // kernel writes split partials even with one split, and the combine
+  // kernel writes the fp32 output from them.
+  int32_t part_out;
 };
 
 // Fewest KV tiles a split keeps (the automatic split heuristic).
@@ -808,7 +812,7 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : 2) void fa2_fwd_kernel(KArg
   }
 
   const float l_tot = sum_xor32(l_run);
-  if (S == 1) {
+  if (S == 1 && !a.part_out) {
     if (qrow < w.Lq) {
       const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
       const int64_t base = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + hi * 4;
@@ -864,7 +868,7 @@ constexpr int kCombineRows = kThreads / (D / 4);  // rows per workgroup
 template <int DT, int D, int MODE>
 __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   const int S = launch_splits(a);
-  if (S <= 1) return;  // the forward kernel wrote the output
+  if (S <= 1 && !a.part_out) return;  // the forward kernel wrote the output
   const Work w = decode_work<MODE>(a, blockIdx.x);
   if (!w.valid) return;
   constexpr int kTPR = D / 4;  // threads per row, 4 floats each
@@ -955,6 +959,41 @@ __device__ __forceinline__ int plan_items(const KArgs& a, int nq) {
 }
 __device__ __forceinline__ int plan_cost_block(const KArgs& a, int j, int nq) {
   return a.qpair ? min(2 * j + 1, nq - 1) : j;
+}
+
+// fp32 -> fp16 copies of q, k and v, rounded as the 16-bit kernels round
+// fp32 operands (to16): flash_attention_v2 converts its fp32 inputs to fp16
+// before every product (attention.py:547, 569, 621).  Segment i copies a
+// [n0][n1][n2][D] view (element strides s0, s1, s2; dims contiguous) into a
+// contiguous buffer; D / 8 threads per row, 8 elements each, one launch for
+// all three.
+struct ConvSeg {
+  const float* src;
+  int64_t s0, s1, s2;
+  int32_t n1, n2;
+  int64_t rows;
+  uint16_t* dst;
+};
+struct ConvArgs {
+  ConvSeg seg[3];
+};
+constexpr int kConvThreads = 256;
+template <int D>
+__global__ __launch_bounds__(kConvThreads) void fa2_to_f16_kernel(ConvArgs c) {
+  constexpr int kTPR = D / 8;
+  int64_t row = (static_cast<int64_t>(blockIdx.x) * kConvThreads + threadIdx.x) / kTPR;
+  const int col = static_cast<int>(threadIdx.x % kTPR) * 8;  // kConvThreads % kTPR == 0
+  int i = 0;
+  while (i < 3 && row >= c.seg[i].rows) row -= c.seg[i++].rows;
+  if (i == 3) return;
+  const ConvSeg& g = c.seg[i];
+  const int64_t i2 = row % g.n2, r1 = row / g.n2;
+  const int64_t i1 = r1 % g.n1, i0 = r1 / g.n1;
+  const float* p = g.src + i0 * g.s0 + i1 * g.s1 + i2 * g.s2 + col;
+  Raw8<FA2_DTYPE_F32> r;
+  r.w[0] = *reinterpret_cast<const u32x4*>(p);
+  r.w[1] = *reinterpret_cast<const u32x4*>(p + 4);
+  *reinterpret_cast<u32x4*>(g.dst + row * D + col) = to16<FA2_DTYPE_F32>(r);
 }
 
 template <int MODE>

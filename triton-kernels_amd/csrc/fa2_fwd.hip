@@ -35,6 +35,11 @@
 #ifndef FA2_SHORT
 #define FA2_SHORT 1
 #endif
+// 1: fp32 tensors of flash_attention_v2 (fp16 rounding) run the 16-bit
+// kernels on fp16 copies (see make_plan); 0: the register-staged kernel
+#ifndef FA2_F32_CONV
+#define FA2_F32_CONV 1
+#endif
 // 1: ragged/paged two-head launches claim units from per-XCD counters
 // (KArgs::claim); 0: the static round walk
 #ifndef FA2_PP_CLAIM
@@ -102,12 +107,14 @@ struct Plan {
   int block_rows;   // rows per q-block of the launched kernel
   bool dec;         // packed fp16/bf16: the decode kernel
   bool f32;         // fp32 arithmetic: the fp32-MFMA kernel
+  bool conv;        // fp32 tensors with the reference's fp16 rounding: fp16 copies in the
+                    // workspace, the 16-bit kernels, partials and an fp32 combine
   bool plan;        // ragged/paged: the plan kernel orders the work list
   bool dev_splits;  // ... and lowers the automatic split count (KArgs::split_count)
   bool buf;         // paged: every row of the pool has a 31-bit byte offset
   int64_t max_wgs;  // cap on the persistent grid (0: none)
   uint32_t pool_bytes_k, pool_bytes_v;
-  size_t off_work, off_count, off_ml, off_o, total;
+  size_t off_work, off_count, off_ml, off_o, off_cq, off_ck, off_cv, total;
 };
 
 // K/V tiles are read through buffer descriptors.  Dense and ragged tiles, and
@@ -210,8 +217,18 @@ int64_t kv_upper_bound(const fa2_params* p) {
   return ub;
 }
 
-int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
+int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv = true) {
   const int64_t nqb = cdiv(p->q_len, kBM);
+  // fp32 tensors of flash_attention_v2, whose reference rounds every operand
+  // to fp16 (attention.py:547, 569, 621) and keeps fp32 partials that a
+  // second kernel merges into the output (:636-746): dense and ragged calls
+  // at head_dim 64/128 convert q, k and v to fp16 copies in the workspace
+  // and run the 16-bit kernels, which write fp32 partials even unsplit;
+  // the combine kernel writes the fp32 output.  Paged pools are not copied.
+  pl->conv = FA2_F32_CONV && allow_conv && p->dtype == FA2_DTYPE_F32 &&
+             p->arith != FA2_ARITH_FP32 && p->layout != FA2_LAYOUT_PAGED &&
+             fast_dim(p->head_dim);
+  const bool half = p->dtype != FA2_DTYPE_F32 || pl->conv;  // the 16-bit kernels
   if (p->layout == FA2_LAYOUT_DENSE)
     pl->work_ub = nqb * p->batch;
   else if (p->layout == FA2_LAYOUT_RAGGED)
@@ -225,7 +242,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
   pl->grid_x = cdiv(pl->npairs, kXcds) * kXcds * group;
   if (pl->grid_x > INT32_MAX || pl->npairs > INT32_MAX) return FA2_ERR_TOO_LARGE;
   pl->dim = tile_dim(p->head_dim);
-  pl->pp = FA2_PP && p->dtype != FA2_DTYPE_F32 && group % 2 == 0 && fast_dim(p->head_dim);
+  pl->pp = FA2_PP && half && group % 2 == 0 && fast_dim(p->head_dim);
   pl->grid_pp = cdiv(pl->npairs, kXcds) * kXcds * cdiv(group, 2);
 
   // A call whose regular grid fills at most half of the CUs and whose KV
@@ -286,6 +303,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device) {
                             (p->layout == FA2_LAYOUT_PAGED && nqb >= 4) ||
                             (p->layout == FA2_LAYOUT_RAGGED && p->batch > 0 &&
                              p->q_len >= 4 * kBM * p->batch);
+  // (the partial slots of a two-head unit assume two heads, not two q-blocks)
   pl->qpair = FA2_PP && p->dtype != FA2_DTYPE_F32 && group == 1 && fast_dim(p->head_dim) &&
               splits == 1 && many_qblocks && !pl->shortk;
   if (pl->shortk) pl->pp = false;
@@ -339,13 +357,25 @@ int finish_plan(const fa2_params* p, Plan* pl) {
   off = (off + 255) & ~size_t(255);
   pl->off_count = off;  // the item count, the split count, the claim counters at kClaimOffset
   if (p->layout != FA2_LAYOUT_DENSE) off += 256;
+  const bool parts = splits > 1 || pl->conv;
   pl->off_ml = off;
-  if (splits > 1)
+  if (parts)
     off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * 2 * sizeof(float);
   off = (off + 255) & ~size_t(255);
   pl->off_o = off;
-  if (splits > 1)
+  if (parts)
     off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * pl->dim * sizeof(float);
+  // fp16 copies: q [B][Hq][Lq][D] or [Tq][Hq][D], k and v likewise
+  const int64_t qrows = p->layout == FA2_LAYOUT_DENSE ? p->batch * p->q_len : p->q_len;
+  const int64_t kvrows = p->layout == FA2_LAYOUT_DENSE ? p->batch * p->kv_len : p->kv_len;
+  auto copy = [&](size_t& at, int64_t rows, int64_t heads) {
+    off = (off + 255) & ~size_t(255);
+    at = off;
+    if (pl->conv) off += static_cast<size_t>(rows) * heads * p->head_dim * 2;
+  };
+  copy(pl->off_cq, qrows, p->q_heads);
+  copy(pl->off_ck, kvrows, p->kv_heads);
+  copy(pl->off_cv, kvrows, p->kv_heads);
   pl->total = off;
   return FA2_OK;
 }
@@ -364,6 +394,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   pl->dim = tile_dim(p->head_dim);
   pl->dec = p->dtype != FA2_DTYPE_F32 && fast_dim(p->head_dim);
   pl->f32 = p->dtype == FA2_DTYPE_F32;  // decode's reference computes fp32 in fp32
+  pl->conv = false;
   pl->block_rows = pl->dec ? kDecRows : kBM;
   const int64_t nqb = cdiv(pl->rows, pl->block_rows);
   pl->work_ub = nqb * p->batch;
@@ -512,10 +543,12 @@ int launch_typed(KArgs a, const Plan& pl, hipStream_t st) {
     }
   }
   if (generic) FA2_LAUNCH_BUF(fa2_fwd_kernel, grid, dim3(kThreads));
-  if (pl.splits > 1) {
-    hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
-                       dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads), 0, st,
+  const dim3 cgrid(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>));
+  if (a.part_out) {  // fp32 output of fp16 copies (Plan::conv)
+    hipLaunchKernelGGL((fa2_combine_kernel<FA2_DTYPE_F32, D, MODE>), cgrid, dim3(kThreads), 0, st,
                        a);
+  } else if (pl.splits > 1) {
+    hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), cgrid, dim3(kThreads), 0, st, a);
   }
   return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
 }
@@ -591,7 +624,9 @@ int workspace_size(const fa2_params* p, size_t* bytes, bool packed) {
   return FA2_OK;
 }
 
-int run(const fa2_params* p, void* stream, bool packed) {
+// allow_conv = false: fp32 tensors keep the register-staged kernel (no
+// fp16 copies in the workspace; fa2_fwd_noalloc when they do not fit)
+int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) {
   int s = packed ? validate_decode(p) : validate(p);
   if (s != FA2_OK) return s;
   if (empty_problem(p)) return FA2_OK;
@@ -600,7 +635,7 @@ int run(const fa2_params* p, void* stream, bool packed) {
     return FA2_ERR_ALIGNMENT;
   Plan pl;
   s = packed ? make_plan_packed(p, &pl, p->num_splits == 0)
-             : make_plan(p, &pl, p->num_splits == 0);
+             : make_plan(p, &pl, p->num_splits == 0, allow_conv);
   if (s != FA2_OK) return s;
   if (pl.total > 0 && (!p->workspace || p->workspace_bytes < pl.total)) return FA2_ERR_WORKSPACE;
 
@@ -645,14 +680,72 @@ int run(const fa2_params* p, void* stream, bool packed) {
   a.work = pl.plan ? reinterpret_cast<const int2*>(ws + pl.off_work) : nullptr;
   a.work_count = pl.plan ? reinterpret_cast<const int32_t*>(ws + pl.off_count) : nullptr;
   a.split_count = pl.dev_splits ? reinterpret_cast<int32_t*>(ws + pl.off_count) + 1 : nullptr;
-  a.part_ml = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
-  a.part_o = pl.splits > 1 ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
+  const bool parts = pl.splits > 1 || pl.conv;
+  a.part_ml = parts ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
+  a.part_o = parts ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
   a.part_rows = pl.part_rows;
   a.pack_m = packed ? static_cast<int32_t>(p->q_len) : 0;
   a.dv = static_cast<int32_t>(p->head_dim);
   a.spin_cap = p->decode_spin_cap > 0 ? p->decode_spin_cap : kDecSpinCap;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (pl.conv) {
+    // q, k, v -> contiguous fp16 copies ([B][H][L][D] dense, [T][H][D]
+    // ragged), then the 16-bit kernels with an fp32 combine
+    const bool dense = p->layout == FA2_LAYOUT_DENSE;
+    const int64_t D = p->head_dim;
+    uint16_t* cq = reinterpret_cast<uint16_t*>(ws + pl.off_cq);
+    uint16_t* ck = reinterpret_cast<uint16_t*>(ws + pl.off_ck);
+    uint16_t* cv = reinterpret_cast<uint16_t*>(ws + pl.off_cv);
+    auto seg = [&](const void* src, int64_t sb, int64_t sh, int64_t ss, int64_t len,
+                   int64_t heads, uint16_t* dst) {
+      ConvSeg g;
+      g.src = static_cast<const float*>(src);
+      if (dense) {  // [B][H][L]
+        g.s0 = sb; g.s1 = sh; g.s2 = ss;
+        g.n1 = static_cast<int32_t>(heads);
+        g.n2 = static_cast<int32_t>(len);
+        g.rows = p->batch * heads * len;
+      } else {  // [T][H]
+        g.s0 = 0; g.s1 = ss; g.s2 = sh;
+        g.n1 = static_cast<int32_t>(len);
+        g.n2 = static_cast<int32_t>(heads);
+        g.rows = len * heads;
+      }
+      g.dst = dst;
+      return g;
+    };
+    ConvArgs c;
+    c.seg[0] = seg(p->q, p->q_sb, p->q_sh, p->q_ss, p->q_len, p->q_heads, cq);
+    c.seg[1] = seg(p->k, p->k_sb, p->k_sh, p->k_ss, p->kv_len, p->kv_heads, ck);
+    c.seg[2] = seg(p->v, p->v_sb, p->v_sh, p->v_ss, p->kv_len, p->kv_heads, cv);
+    const int64_t rows = c.seg[0].rows + c.seg[1].rows + c.seg[2].rows;
+    const int64_t blocks = cdiv(rows * (D / 8), kConvThreads);
+    if (blocks > INT32_MAX) return FA2_ERR_TOO_LARGE;
+    if (blocks > 0) {
+      if (D == 64)
+        hipLaunchKernelGGL((fa2_to_f16_kernel<64>), dim3(static_cast<uint32_t>(blocks)),
+                           dim3(kConvThreads), 0, st, c);
+      else
+        hipLaunchKernelGGL((fa2_to_f16_kernel<128>), dim3(static_cast<uint32_t>(blocks)),
+                           dim3(kConvThreads), 0, st, c);
+    }
+    auto strides = [&](int64_t len, int64_t heads, int64_t& sb, int64_t& sh, int64_t& ss) {
+      if (dense) {
+        sb = heads * len * D; sh = len * D; ss = D;
+      } else {
+        sb = 0; sh = D; ss = heads * D;
+      }
+    };
+    a.q = cq;
+    a.k = ck;
+    a.v = cv;
+    strides(p->q_len, p->q_heads, a.q_sb, a.q_sh, a.q_ss);
+    strides(p->kv_len, p->kv_heads, a.k_sb, a.k_sh, a.k_ss);
+    strides(p->kv_len, p->kv_heads, a.v_sb, a.v_sh, a.v_ss);
+    a.part_out = 1;
+    return launch_dim<FA2_DTYPE_F16>(pl.dim, p->layout, a, pl, st);
+  }
   switch (p->dtype) {
     case FA2_DTYPE_F16: return launch_dim<FA2_DTYPE_F16>(pl.dim, p->layout, a, pl, st);
     case FA2_DTYPE_BF16: return launch_dim<FA2_DTYPE_BF16>(pl.dim, p->layout, a, pl, st);
@@ -710,12 +803,18 @@ extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
   Plan pl;
   s = make_plan(&c, &pl, c.num_splits == 0);
   if (s != FA2_OK) return s;
+  // fp32 tensors whose fp16 copies do not fit keep the register-staged kernel
+  const bool conv = !(pl.conv && pl.total > cap);
+  if (!conv) {
+    s = make_plan(&c, &pl, c.num_splits == 0, false);
+    if (s != FA2_OK) return s;
+  }
   if (pl.total > cap) {
     if (p->num_splits != 0) return FA2_ERR_SCRATCH;
     // fewer automatic splits until the partials fit
     for (int sp = pl.splits - 1; sp >= 1 && pl.total > cap; --sp) {
       c.num_splits = sp;
-      s = make_plan(&c, &pl, false);
+      s = make_plan(&c, &pl, false, conv);
       if (s != FA2_OK) return s;
     }
     if (pl.total > cap) return FA2_ERR_SCRATCH;
@@ -724,7 +823,7 @@ extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
   if (!ws) return FA2_ERR_HIP;
   c.workspace = ws;
   c.workspace_bytes = cap;
-  return run(&c, stream, false);
+  return run(&c, stream, false, conv);
 }
 
 extern "C" int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes) {

@@ -736,7 +736,7 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : FA2_LDS_OCCUPANCY) void fa2
   }
 
   const float l_tot = sum_xor32(l_run);
-  if (S == 1) {
+  if (S == 1 && !a.part_out) {
     static_assert(kWaves * OStage<D>::kBytes <= sizeof(lds), "O staging exceeds LDS");
     __syncthreads();  // the last tile's buffers may still be read by other waves
     const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference

@@ -537,7 +537,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       }
       if (dyn) rn = claim_read();
       has_next = next_unit(rn, nxt);
-      pre_next = has_next && nxt.T > 0 && S == 1;
+      // (not when this unit's rows go out as partials: the waits after the
+      // prefetch count the staged output stores)
+      pre_next = has_next && nxt.T > 0 && S == 1 && !a.part_out;
       // Q of the next unit: this group's last S is done
       if (pre_next) load_q(nxt);
       phase_v(T - 1);
@@ -574,7 +576,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
 
     if (u.hok) {
       const float l_tot = sum_xor32(l_run);
-      if (S == 1) {
+      if (S == 1 && !a.part_out) {
         const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
         const int nrows = max(0, min(w.Lq - wq_first, kWaveRows));
         const __amdgpu_buffer_rsrc_t out = make_rsrc_uniform(
