@@ -182,8 +182,11 @@ enum fa2_kernel {
 
 /* Bytes of device workspace fa2_fwd needs for `p` (0 is possible).
  * Replaces the reference's per-call torch.empty of running_sum/max/acc
- * (attention.py:852-864).  Host-only: touches no device state except a
- * one-time, cached query of the current device's compute-unit count. */
+ * (attention.py:852-864).  fp32 tensors with FA2_ARITH_REFERENCE at
+ * head_dim 64/128 (dense, ragged) also hold fp16 copies of q, k and v there,
+ * as the reference rounds every fp32 operand to fp16.  Host-only: touches
+ * no device state except a one-time, cached query of the current device's
+ * compute-unit count. */
 int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes);
 
 /* Validate `p` and enqueue the forward pass on `stream` (a hipStream_t;
@@ -198,8 +201,9 @@ int fa2_fwd(const fa2_params* p, void* stream);
  * work list and the split-KV partials live in a static device array of
  * FA2_NOALLOC_SCRATCH_BYTES that the library holds on every device it runs on
  * until the process ends.  Automatic splits (num_splits = 0) are reduced until
- * the call fits that array; a call that still does not fit, or a forced
- * num_splits that does not, returns FA2_ERR_SCRATCH before any launch.  The
+ * the call fits that array, and fp32 tensors whose fp16 copies do not fit
+ * run the register-staged kernel instead; a call that still does not fit, or
+ * a forced num_splits that does not, returns FA2_ERR_SCRATCH before any launch.  The
  * entry point calls no allocating routine.  Every call on one device shares
  * that device's array: calls that overlap in time on one device (e.g. on two
  * streams) race and give wrong results; serialise them.  Otherwise the same
