@@ -207,8 +207,8 @@ int fa2_fwd(const fa2_params* p, void* stream);
  * entry point calls no allocating routine.  Every call on one device shares
  * that device's array: calls that overlap in time on one device (e.g. on two
  * streams) race and give wrong results; serialise them.  Otherwise the same
- * contract and results as fa2_fwd (bit-identical when the split factor is the
- * same). */
+ * contract and results as fa2_fwd (bit-identical when the split factor and
+ * the kernel are the same). */
 #define FA2_NOALLOC_SCRATCH_BYTES (32u << 20)
 int fa2_fwd_noalloc(const fa2_params* p, void* stream);
 

@@ -105,6 +105,22 @@ def test_v1_fp32_graph():
     _replay_matches(fn, [q, k, v], [None, _perturbed([q, k, v], 4)])
 
 
+@pytest.mark.parametrize("layout", ["dense", "ragged"])
+def test_v2_fp32_graph(layout):
+    """fp32 tensors of flash_attention_v2: the fp16 conversion, the 16-bit
+    forward writing partials and the fp32 combine, in one graph."""
+    from kernels import flash_attention_v2
+    case = make_case(3, 8, 2, 128, "self", torch.float32, layout, 9350, q_range=(100, 700),
+                     dense_q_range=(400, 400))
+    q, k, v, kw = pack(case, layout, device=DEV)
+    print(f"graph v2 fp32 {layout}", flush=True)
+
+    def fn(q, k, v):
+        return flash_attention_v2(q, k, v, is_causal=True, **kw)
+
+    _replay_matches(fn, [q, k, v], [None, _perturbed([q, k, v], 6), None])
+
+
 @pytest.mark.parametrize("spec", [False, True])
 def test_decode_graph(spec):
     from kernels import decode_attention, speculative_decode_attention
