@@ -134,25 +134,29 @@ def test_claimed_units_mixed_lengths(layout, mask, dtype):
 
 
 @pytest.mark.parametrize("layout", ["ragged", "paged"])
-def test_claimed_units_empty_kv(layout):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_claimed_units_empty_kv(layout, dtype):
     """Sequences with no keys give units of no tiles, which claim through a
     barrier of their own: their rows are NaN (0/0, as the reference), and
-    every other sequence's rows equal, bit for bit, a call without them."""
+    every other sequence's rows equal, bit for bit, a call without them.
+    fp32 ragged runs the 16-bit kernels on fp16 copies with fp32 partials and
+    combine; fp32 paged the register-staged kernel."""
     from kernels.attention import flash_attention_v2
     ql = [200, 64, 300, 129, 90, 260, 40, 500]
     kl = [300, 1, 700, 65, 1, 128, 64, 900]
     empty = [1, 4]
-    case = make_case(len(ql), 8, 2, 128, "cross", torch.bfloat16, layout, 4500, q_lens=ql,
+    case = make_case(len(ql), 8, 2, 128, "cross", dtype, layout, 4500, q_lens=ql,
                      kv_lens=kl)
     keep = [b for b in range(len(ql)) if b not in empty]
-    sub = make_case(len(keep), 8, 2, 128, "cross", torch.bfloat16, layout, 4500,
+    sub = make_case(len(keep), 8, 2, 128, "cross", dtype, layout, 4500,
                     q_lens=[ql[b] for b in keep], kv_lens=[kl[b] for b in keep])
     sub.qs[:] = [case.qs[b] for b in keep]
     sub.ks[:] = [case.ks[b] for b in keep]
     sub.vs[:] = [case.vs[b] for b in keep]
-    print(f"claims empty kv {layout}", flush=True)
-    ref, rkw = run(sub, layout, False)
+    print(f"claims empty kv {layout} {dtype}", flush=True)
+    ref, rkw = run(sub, layout, False, num_splits=1)
     ref = unpack(sub, layout, ref, rkw)
+    view = torch.int32 if dtype == torch.float32 else torch.int16
     for wgs in (0, 8, 11):
         q, k, v, kw = pack(case, layout, device=DEV)
         if layout == "ragged":
@@ -166,13 +170,13 @@ def test_claimed_units_empty_kv(layout):
             lens = torch.tensor(kl, dtype=torch.int32)
             lens[empty] = 0
             kw["kv_indptr"] = lens.to(DEV)
-        out = flash_attention_v2(q, k, v, is_causal=False, max_workgroups=wgs,
+        out = flash_attention_v2(q, k, v, is_causal=False, max_workgroups=wgs, num_splits=1,
                                  kernel="regular", **kw).cpu()
         outs = unpack(case, layout, out, kw)
         for b in empty:
             assert torch.isnan(outs[b].float()).all(), (wgs, b)
         for i, b in enumerate(keep):
-            assert torch.equal(outs[b].view(torch.int16), ref[i].view(torch.int16)), (wgs, b)
+            assert torch.equal(outs[b].view(view), ref[i].view(view)), (wgs, b)
 
 
 def test_max_workgroups_only_caps():
