@@ -439,8 +439,9 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   // was 7 % of the step.)
   pl->plan = p->layout != FA2_LAYOUT_DENSE;
   pl->dev_splits = false;
+  const int64_t resident = pl->dec ? 1 : (pl->dim > 128 ? 1 : 2);  // workgroups per CU
   if (pl->plan && (pl->dec || pl->f32) && query_device &&
-      pl->grid_x * splits <= cu_count_current_device() * (pl->dec ? 1 : 2))
+      pl->grid_x * splits <= cu_count_current_device() * resident)
     pl->plan = false;
   return finish_plan(p, pl);
 }
