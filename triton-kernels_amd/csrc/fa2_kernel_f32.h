@@ -7,8 +7,9 @@
 //   decode_attention (kernels/decode.py:84, 92-160) and
 //   speculative_decode_attention (kernels/speculative_decode.py:91-175):
 //     q, k, v in fp32, weights in fp32 (packed-head mode, KArgs::pack_m).
-// flash_attention_v2 rounds fp32 operands to fp16 (attention.py:547-633) and
-// keeps the register-staged kernel of fa2_device.h.
+// flash_attention_v2 rounds fp32 operands to fp16 (attention.py:547-633): it
+// runs the 16-bit kernels on fp16 copies, or the register-staged kernel of
+// fa2_device.h.
 //
 // Layout (one workgroup = 4 waves, 128 query rows, 32 per wave; KV tiles of
 // 64 keys, one K and one V tile in LDS):
