@@ -49,7 +49,10 @@ import torch
 import torch.nn.functional as F
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# FA2_ORACLE_LIBRARY selects a prebuilt oracle library (the sanitizer build,
+# oracle/_san/liboracle.so); build() then leaves it as it is.
+_LIB_PATH = os.environ.get("FA2_ORACLE_LIBRARY") or os.path.join(_HERE, "liboracle.so")
+_OVERRIDDEN = bool(os.environ.get("FA2_ORACLE_LIBRARY"))
 _lib = None
 _lock = threading.Lock()
 
@@ -90,6 +93,8 @@ class _Args(ctypes.Structure):
 
 def build(force: bool = False) -> str:
     """Compile ``liboracle.so`` with gcc (oracle/Makefile)."""
+    if _OVERRIDDEN:
+        return _LIB_PATH
     if force or not os.path.exists(_LIB_PATH):
         subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"], check=True)
     return _LIB_PATH

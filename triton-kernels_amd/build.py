@@ -77,13 +77,43 @@ def build_ext(verbose: bool = False) -> str:
     return out
 
 
-def build(verbose: bool = False) -> str:
+# Host-sanitized build of the same library (AddressSanitizer + UBSan on the
+# host code only: parameter checks, plans, workspace sizing).  Its device code
+# is the regular build's; it is for CPU tests that call the host half of the C
+# ABI under the clang ASan runtime (tests/test_sanitizers.py), never for GPU runs.
+SAN_DIR = os.path.join(HERE, "_san")
+SAN_OUT = os.path.join(SAN_DIR, "libfa2.so")
+SAN_HOST_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_host", "-g",
+    "-Xarch_host", "-O1",
+]
+
+
+def build(verbose: bool = False, sanitize: bool = False) -> str:
+    """Compile libfa2.so and the launch extension; with ``sanitize`` also the
+    host-sanitized libfa2.so (in parallel with the regular one)."""
     tmp = OUT + ".tmp"
+    san = None
+    if sanitize:
+        os.makedirs(SAN_DIR, exist_ok=True)
+        san_cmd = [HIPCC] + FLAGS + SAN_HOST_FLAGS + SOURCES + ["-o", SAN_OUT + ".tmp"]
+        if verbose:
+            print(" ".join(san_cmd), flush=True)
+        san = subprocess.Popen(san_cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     _run([HIPCC] + FLAGS + SOURCES + ["-o", tmp], verbose, "hipcc")
     os.replace(tmp, OUT)
     build_ext(verbose)
+    if san is not None:
+        log, _ = san.communicate()
+        if san.returncode != 0:
+            raise RuntimeError(f"hipcc (sanitized host build) failed ({san.returncode}):\n{log}")
+        os.replace(SAN_OUT + ".tmp", SAN_OUT)
     return OUT
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, sanitize="--sanitize" in sys.argv[1:]))

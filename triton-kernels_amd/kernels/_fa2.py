@@ -12,7 +12,9 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libfa2.so")
+# FA2_LIBRARY selects another build of the same library, such as the
+# host-sanitized one that build.py writes to triton-kernels_amd/_san/.
+LIB_PATH = os.environ.get("FA2_LIBRARY") or os.path.join(_HERE, "libfa2.so")
 
 LAYOUT_DENSE, LAYOUT_RAGGED, LAYOUT_PAGED = 0, 1, 2
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
