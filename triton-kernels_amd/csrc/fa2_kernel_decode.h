@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
 
   if (wave >= 4) {
     // ---- producers ---------------------------------------------------------
-    using Ld = DirectLoader<D, MODE, BUF, DT>;
+    using Ld = DirectLoader<D, MODE, BUF, DT, kWaves, /*NT=*/true>;  // K/V are read once
     const Ld ld(a, wave - 4, lane);
     // paged caches with whole pages per wave and tile: the block-table
     // entries of tile i + 1 are read while tile i is issued

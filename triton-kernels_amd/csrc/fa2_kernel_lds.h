@@ -78,17 +78,35 @@ __device__ __forceinline__ lds_char_t* to_lds(void* p) {
 //     the descriptor words and restore spilled SGPRs) followed by a vector
 //     memory instruction that reads that SGPR: 5 wait states (s_nop 4);
 //   * an SALU write of M0 followed by a load to LDS: 1 (s_nop 0).
+//
+// NT selects the non-temporal cache policy (`nt`), for data that the launch
+// reads once (decode's K/V: +2 % on d1, d2 and s1).  Prefill keeps the default:
+// its K/V tiles are read again by the other units of a kv head from L2
+// (`nt` there measured c3 -4.6 %, c2 -1.6 %).
+template <bool NT = false>
 __device__ __forceinline__ void dma_buffer_x4(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(rsrc),
-                 "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
+  if constexpr (NT)
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+                 :
+                 : "v"(voff), "s"(rsrc),
+                   "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
+  else
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc),
+                   "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
 }
 
+template <bool NT = false>
 __device__ __forceinline__ void dma_global_x4(const void* gptr, uint32_t lds_addr) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(gptr), "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
+  if constexpr (NT)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(gptr), "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
+  else
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gptr), "{m0}"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr))));
 }
 
 // One 32-bit read of read-only global memory at a wave-uniform address through
@@ -125,8 +143,9 @@ __device__ __forceinline__ lds_char_t* lds_ptr(uint32_t addr) {
   return (lds_char_t*)(static_cast<uintptr_t>(addr));
 }
 
-// Tile loads shared by NW waves (each issues kInstr 1 KiB instructions).
-template <int D, int MODE, bool BUF, int DT, int NW = kWaves>
+// Tile loads shared by NW waves (each issues kInstr 1 KiB instructions);
+// NT: non-temporal loads (see dma_buffer_x4).
+template <int D, int MODE, bool BUF, int DT, int NW = kWaves, bool NT = false>
 struct DirectLoader {
   using G = std::conditional_t<DT == FA2_DTYPE_F32, SwzGeo32<D>, SwzGeo<D>>;
   static constexpr int kEB = Elt<DT>::kBytes;
@@ -274,7 +293,7 @@ struct DirectLoader {
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
       const uint32_t off = j * kRPI * rsb + src_off<IS_V>(j);
-      dma_buffer_x4(rsrc, ldst + j * 1024,
+      dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
                     (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
     }
   }
@@ -315,7 +334,7 @@ struct DirectLoader {
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
           const uint32_t off = j * kRPI * rsb + src_off<IS_V>(j);
-          dma_buffer_x4(rsrc, ldst + j * 1024,
+          dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
                         (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
         }
       } else if (a.page_size % kRPI == 0) {
@@ -325,7 +344,7 @@ struct DirectLoader {
           const int prow = paged_row_uniform(a, tbl, ts, w.b, min(n0, w.Lk - 1));
           const u32x4 rsrc = page_rsrc(a, pool, prow, kRPI, rsb);
           const uint32_t off = src_off<IS_V>(j);
-          dma_buffer_x4(rsrc, ldst + j * 1024,
+          dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
                         (n0 + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
         }
       } else if constexpr (BUF) {
@@ -337,7 +356,7 @@ struct DirectLoader {
           const int nc = min(n, w.Lk - 1);
           const uint32_t prow = static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
           const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
-          dma_buffer_x4(rsrc, ldst + j * 1024,
+          dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
                         (n < w.Lk && cok<IS_V>(j)) ? prow * rsb + col : 0xFFFFFF00u);
         }
       } else {
@@ -350,7 +369,7 @@ struct DirectLoader {
           // that meets zero q dims, or V columns that are never stored)
           const uint32_t col =
               cok<IS_V>(j) ? (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16 : 0u;
-          dma_global_x4(pool + prow * rs * kEB + col, ldst + j * 1024);
+          dma_global_x4<NT>(pool + prow * rs * kEB + col, ldst + j * 1024);
         }
       }
     } else {
@@ -360,7 +379,7 @@ struct DirectLoader {
           static_cast<const char*>(src) + (base + static_cast<int64_t>(k0) * rs) * kEB, lim);
 #pragma unroll
       for (int j = 0; j < kInstr; ++j)
-        dma_buffer_x4(rsrc, ldst + j * 1024,
+        dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
                       cok<IS_V>(j) ? src_off<IS_V>(j) : 0xFFFFFF00u);
     }
   }
