@@ -294,7 +294,7 @@ struct DirectLoader {
     for (int j = 0; j < kInstr; ++j) {
       const uint32_t off = j * kRPI * rsb + src_off<IS_V>(j);
       dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
-                    (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
+                        (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
     }
   }
 
@@ -335,7 +335,7 @@ struct DirectLoader {
         for (int j = 0; j < kInstr; ++j) {
           const uint32_t off = j * kRPI * rsb + src_off<IS_V>(j);
           dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
-                        (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
+                            (n0 + j * kRPI + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
         }
       } else if (a.page_size % kRPI == 0) {
 #pragma unroll
@@ -345,7 +345,7 @@ struct DirectLoader {
           const u32x4 rsrc = page_rsrc(a, pool, prow, kRPI, rsb);
           const uint32_t off = src_off<IS_V>(j);
           dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
-                        (n0 + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
+                            (n0 + lane_row() < w.Lk && cok<IS_V>(j)) ? off : 0xFFFFFF00u);
         }
       } else if constexpr (BUF) {
         const u32x4 rsrc = rsrc_words(pool, IS_V ? a.pool_bytes_v : a.pool_bytes_k);
@@ -357,7 +357,7 @@ struct DirectLoader {
           const uint32_t prow = static_cast<uint32_t>(paged_row(tbl, ts, w.b, nc, a.page_size));
           const uint32_t col = (slot_of() ^ (IS_V ? G::v(r) : G::k(r))) * 16;
           dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
-                        (n < w.Lk && cok<IS_V>(j)) ? prow * rsb + col : 0xFFFFFF00u);
+                            (n < w.Lk && cok<IS_V>(j)) ? prow * rsb + col : 0xFFFFFF00u);
         }
       } else {
 #pragma unroll
@@ -380,7 +380,7 @@ struct DirectLoader {
 #pragma unroll
       for (int j = 0; j < kInstr; ++j)
         dma_buffer_x4<NT>(rsrc, ldst + j * 1024,
-                      cok<IS_V>(j) ? src_off<IS_V>(j) : 0xFFFFFF00u);
+                          cok<IS_V>(j) ? src_off<IS_V>(j) : 0xFFFFFF00u);
     }
   }
 };
