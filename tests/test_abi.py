@@ -73,6 +73,8 @@ def rc_fwd(p):
     ("max_workgroups", -1, 5), ("kv_len_max", -1, 5), ("arith", 2, 3), ("arith", -1, 3),
     ("decode_spin_cap", -1, 5), ("kernel", 3, 5), ("kernel", -1, 5),
     ("k_ss", (1 << 24) + 8, 13),  # a 32 MiB+ row stride: tile offsets leave 32 bits
+    ("q_ss", (1 << 24) + 8, 13),  # the same for the q-block offsets of the short kernel
+    ("q_ss", 1 << 26, 13),  # 128 MiB: uint32(q_ss * 2) alone would wrap to 0
 ])
 def test_validation_errors(field, value, code):
     p = dense_params(**{field: value})

@@ -63,8 +63,16 @@ def test_host_code_under_asan_and_ubsan():
         pytest.skip(why)
     assert _instrumented(SAN_FA2), SAN_FA2
     assert _instrumented(SAN_ORACLE), SAN_ORACLE
+    # ASan's runtime must come first among the preloaded libraries; any the
+    # environment already preloads stay after it.  Every GPU is hidden: the
+    # sanitized child must not start the HIP runtime, and its plans then use
+    # the fixed CU-count fallback on any host.
+    pre = os.environ.get("LD_PRELOAD", "")
     env = dict(os.environ,
-               LD_PRELOAD=_asan_runtime(),
+               LD_PRELOAD=_asan_runtime() + (":" + pre if pre else ""),
+               HIP_VISIBLE_DEVICES="-1",
+               CUDA_VISIBLE_DEVICES="-1",
+               ROCR_VISIBLE_DEVICES="-1",
                ASAN_OPTIONS="detect_leaks=0:halt_on_error=1",
                UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
                FA2_LIBRARY=SAN_FA2,

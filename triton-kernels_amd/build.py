@@ -104,14 +104,24 @@ def build(verbose: bool = False, sanitize: bool = False) -> str:
         if verbose:
             print(" ".join(san_cmd), flush=True)
         san = subprocess.Popen(san_cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    _run([HIPCC] + FLAGS + SOURCES + ["-o", tmp], verbose, "hipcc")
-    os.replace(tmp, OUT)
-    build_ext(verbose)
+    try:
+        _run([HIPCC] + FLAGS + SOURCES + ["-o", tmp], verbose, "hipcc")
+        os.replace(tmp, OUT)
+    finally:
+        log = san.communicate()[0] if san is not None else ""
+    # Neither of these is needed at run time (the wrapper falls back to the C
+    # ABI through ctypes; the sanitizer test skips without its library), so a
+    # failure is reported and the build goes on.
+    try:
+        build_ext(verbose)
+    except Exception as e:  # noqa: BLE001 - missing torch headers, compiler errors
+        print(f"warning: launch extension not built: {e}", file=sys.stderr, flush=True)
     if san is not None:
-        log, _ = san.communicate()
         if san.returncode != 0:
-            raise RuntimeError(f"hipcc (sanitized host build) failed ({san.returncode}):\n{log}")
-        os.replace(SAN_OUT + ".tmp", SAN_OUT)
+            print(f"warning: sanitized host build failed ({san.returncode}):\n{log}",
+                  file=sys.stderr, flush=True)
+        else:
+            os.replace(SAN_OUT + ".tmp", SAN_OUT)
     return OUT
 
 

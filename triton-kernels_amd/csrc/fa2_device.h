@@ -1000,7 +1000,7 @@ template <int MODE>
 __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* work,
                                                                 int32_t* work_count) {
   __shared__ int hist[kCostBuckets];
-  __shared__ int scan[kPlanThreads];
+  __shared__ int seq_cost[kPlanThreads];  // the decode fast path's per-sequence costs
   const int tid = threadIdx.x;
   if (a.pack_m > 0 && a.q_len <= a.block_rows && a.batch <= kPlanFastBatch) {
     // Decode with one q-block per sequence and a small batch: item b's
@@ -1010,13 +1010,13 @@ __global__ __launch_bounds__(kPlanThreads) void fa2_plan_kernel(KArgs a, int2* w
       int Lq, Lk;
       seq_lens<MODE>(a, tid, Lq, Lk);
       c = block_cost(a.mask, 0, Lq, Lk, true);
-      scan[tid] = c;
+      seq_cost[tid] = c;
     }
     __syncthreads();
     if (tid < a.batch) {
       int rank = 0;
       for (int u = 0; u < a.batch; ++u) {
-        const int cu = scan[u];
+        const int cu = seq_cost[u];
         rank += (cu > c || (cu == c && u < tid)) ? 1 : 0;
       }
       if (rank < a.work_ub) work[rank] = make_int2(tid, 0);

@@ -12,6 +12,7 @@
 //   * no allocation: the caller passes the workspace.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "fa2_device.h"
@@ -163,10 +164,11 @@ int validate(const fa2_params* p) {
   if (p->batch > lim || p->q_heads > 65536 || p->q_len > lim || p->kv_len > lim ||
       p->page_size > lim)
     return FA2_ERR_TOO_LARGE;
-  // a tile's (or page's) rows are addressed by 32-bit offsets from its first
-  // row: row strides up to 32 MiB
+  // a tile's (or page's, or q-block's) rows are addressed by 32-bit offsets
+  // from its first row: row strides up to 32 MiB
   const int64_t row_lim = int64_t(1) << 25;
-  if (p->k_ss * eb > row_lim || p->v_ss * eb > row_lim || p->o_ss * eb > row_lim)
+  if (p->q_ss * eb > row_lim || p->k_ss * eb > row_lim || p->v_ss * eb > row_lim ||
+      p->o_ss * eb > row_lim)
     return FA2_ERR_TOO_LARGE;
   if (p->max_workgroups < 0 || p->kv_len_max < 0) return FA2_ERR_BAD_SHAPE;
   if (p->arith < FA2_ARITH_REFERENCE || p->arith > FA2_ARITH_FP32) return FA2_ERR_BAD_DTYPE;
@@ -778,18 +780,22 @@ static __device__ __align__(256) unsigned char scratch[FA2_NOALLOC_SCRATCH_BYTES
 namespace fa2 {
 namespace {
 
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
-// This device's copy of `scratch`, or null if the lookup failed.
+// This device's copy of `scratch`, or null if the lookup failed.  Only a
+// successful lookup is kept: a failed one is tried again on the next call.
 void* scratch_current_device() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  std::call_once(g_scratch_once[dev], [dev] {
-    void* ptr = nullptr;
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch_ptr[dev] = ptr;
-  });
-  return g_scratch_ptr[dev];
+  if (void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire)) return ptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (!ptr) {
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  return ptr;
 }
 
 }  // namespace
@@ -802,24 +808,31 @@ extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
   constexpr size_t cap = FA2_NOALLOC_SCRATCH_BYTES;
   fa2_params c = *p;
   Plan pl;
-  s = make_plan(&c, &pl, c.num_splits == 0);
+  // The plan with fp16 copies of fp32 tensors (the faster kernel, and the
+  // one fa2_fwd runs) comes first, with fewer automatic splits until its
+  // workspace fits; fp32 tensors fall back to the register-staged kernel
+  // only when even one split with copies does not fit.
+  auto fit = [&](bool allow_conv) -> int {
+    c = *p;
+    int r = make_plan(&c, &pl, c.num_splits == 0, allow_conv);
+    if (r != FA2_OK) return r;
+    if (p->num_splits == 0)
+      for (int sp = pl.splits - 1; sp >= 1 && pl.total > cap; --sp) {
+        c.num_splits = sp;
+        r = make_plan(&c, &pl, false, allow_conv);
+        if (r != FA2_OK) return r;
+      }
+    return FA2_OK;
+  };
+  bool conv = true;
+  s = fit(true);
   if (s != FA2_OK) return s;
-  // fp32 tensors whose fp16 copies do not fit keep the register-staged kernel
-  const bool conv = !(pl.conv && pl.total > cap);
-  if (!conv) {
-    s = make_plan(&c, &pl, c.num_splits == 0, false);
+  if (pl.total > cap && pl.conv) {
+    conv = false;
+    s = fit(false);
     if (s != FA2_OK) return s;
   }
-  if (pl.total > cap) {
-    if (p->num_splits != 0) return FA2_ERR_SCRATCH;
-    // fewer automatic splits until the partials fit
-    for (int sp = pl.splits - 1; sp >= 1 && pl.total > cap; --sp) {
-      c.num_splits = sp;
-      s = make_plan(&c, &pl, false, conv);
-      if (s != FA2_OK) return s;
-    }
-    if (pl.total > cap) return FA2_ERR_SCRATCH;
-  }
+  if (pl.total > cap) return FA2_ERR_SCRATCH;
   void* ws = scratch_current_device();
   if (!ws) return FA2_ERR_HIP;
   c.workspace = ws;
