@@ -10,7 +10,9 @@ the GPU, sequence by sequence:
    stay within 4x (max) and 2x (RMS) of the error of an fp64 emulation of
    the kernel's rounding (operands and softmax weights rounded as the kernel
    rounds them, output rounded to the dtype) - the reference tolerance alone
-   is nearly vacuous at these lengths;
+   is nearly vacuous at these lengths; for bf16 the same bar also against an
+   emulation of the reference's arithmetic, which rounds bf16 operands and
+   the softmax weights to fp16;
 3. the strict bar against the C oracle (the restatement of the reference
    algorithm, oracle/fa2_oracle.c) on sampled windows - a range of query rows
    of a few query heads of one (sequence, kv head) - with their fp64 truth on
@@ -122,7 +124,10 @@ def test_config_full_size(name, dtype, alignment):
     align = w.causal_alignment if w.is_causal else "top_left"
     o_round, p_round = kernel_rounding(dtype)
     tol = oracle.attn_tolerances(dtype, max(w.kv_lens))
-    kern, emul, truth = [], [], []
+    # bf16: also the reference's own arithmetic (operands and P rounded to
+    # fp16, attention.py:547, 572, 607, 614, 633)
+    ref_arith = dtype == torch.bfloat16
+    kern, emul, truth, emul_ref = [], [], [], []
     for b in range(len(outs)):
         qb, kb, vb = (t.transpose(0, 1) for t in (qs[b], ks[b], vs[b]))  # [H, L, D]
         ob = outs[b].transpose(0, 1).float()
@@ -136,8 +141,15 @@ def test_config_full_size(name, dtype, alignment):
         emul.append(e64.float())
         truth.append(t64)
         del t64, e64
+        if ref_arith:
+            emul_ref.append(gpu_attention(qb, kb, vb, w.is_causal, align, dtype=torch.float64,
+                                          operand_round="f16", p_round="f16").float())
     stats = strict_check(kern, emul, truth, dtype)  # on the GPU
     print(f"  whole output: {stats}", flush=True)
+    if ref_arith:
+        st = strict_check(kern, emul_ref, truth, dtype)
+        print(f"  whole output vs the reference's fp16 arithmetic: {st}", flush=True)
+        del emul_ref
     kern = [t.cpu() for t in kern]
     del emul, truth
 
