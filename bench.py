@@ -176,7 +176,13 @@ def sweep(args) -> int:
     out = open(args.sweep_out, "w") if args.sweep_out else None
     print(f"{'layout':8}{'type':7}{'topo':6}{'mask':8}{'dtype':10}{'Q':>6}{'KV':>6}"
           f"{'v2 us':>10}{'v2 TFLOP/s':>12}{'v1 us':>10}", flush=True)
+    terms = [t for t in (args.sweep_only or "").split(",") if t]
     for pt in W.sweep_points():
+        layout, attn, topo, dt, causal, ql, kl = pt
+        desc = {layout, attn, topo, DTYPE_NAME[dt], "causal" if causal else "full",
+                f"q{ql}", f"kv{ql if attn == 'self' else kl}"}
+        if any(t not in desc for t in terms):
+            continue
         w = W.make_sweep(*pt).to(dev)
         kw = w.kwargs()
         res = {}
@@ -247,6 +253,9 @@ def main(argv=None):
     ap.add_argument("--sweep", action="store_true",
                     help="time the reference benchmark's sweep of shapes instead")
     ap.add_argument("--sweep-out", default=None, help="JSON lines of the sweep")
+    ap.add_argument("--sweep-only", default=None, metavar="TERMS",
+                    help="comma-separated terms (e.g. 'ragged,bf16,q128,kv128'): run only the "
+                         "sweep points whose description holds every term")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes")

@@ -136,7 +136,19 @@ struct KArgs {
   // kernel writes split partials even with one split, and the combine
   // kernel writes the fp32 output from them.
   int32_t part_out;
+  // Split merge inside the forward kernel (no combine launch): one 64-bit
+  // word per unit (part slot), (tag << kMergeCountBits) | count of the
+  // splits that have written their partials.  A word whose tag differs
+  // from merge_tag counts as zero, so the words need no clearing between
+  // calls; the split that completes the count merges the unit's partials
+  // and leaves (tag, 0), so a replay of the same launch (same tag) starts
+  // from zero as well.  null: partials go to the combine kernel.
+  uint64_t* merge_ctr;
+  uint64_t merge_tag;  // nonzero, < 2^kMergeTagBits - 1, distinct per call
 };
+
+constexpr int kMergeCountBits = 24;
+constexpr int kMergeTagBits = 64 - kMergeCountBits;
 
 // Fewest KV tiles a split keeps (the automatic split heuristic).
 constexpr int kMinSplitTiles = 16;
@@ -865,6 +877,90 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : 2) void fa2_fwd_kernel(KArg
 template <int D>
 constexpr int kCombineRows = kThreads / (D / 4);  // rows per workgroup
 
+// Partials of a merge inside the forward kernel are written and read at
+// device scope (relaxed agent-scope atomics: `sc1` loads and stores, coherent
+// across the XCDs' L2 caches without the cache-wide writeback and invalidate
+// of a release/acquire fence); the combine kernel reads them plainly.
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float* p, float x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool DEV>
+__device__ __forceinline__ float ld_part(const float* p) {
+  if constexpr (DEV) return ld_dev(p);
+  else return *p;
+}
+template <bool DEV>
+__device__ __forceinline__ f32x4 ld_part4(const float* p) {
+  if constexpr (DEV) return (f32x4){ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3)};
+  else return *reinterpret_cast<const f32x4*>(p);
+}
+template <bool DEV>
+__device__ __forceinline__ void st_part4(float* p, f32x4 x) {
+  if constexpr (DEV) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st_dev(p + j, x[j]);
+  } else {
+    *reinterpret_cast<f32x4*>(p) = x;
+  }
+}
+
+// Row r, columns col..col+3 of the unit in part slot `unit` (of S splits),
+// written to the output element offset `off`.
+template <int DT, int D, bool DEV = false>
+__device__ __forceinline__ void combine_row(const KArgs& a, int unit, int r, int col, int S,
+                                            int64_t off) {
+  const int64_t G = a.part_slots;
+  const int64_t R = a.part_rows;
+  const float* ml = a.part_ml + (static_cast<int64_t>(unit) * R + r) * 2;
+  const float* po = a.part_o + (static_cast<int64_t>(unit) * R + r) * D + col;
+  const int64_t ml_step = G * R * 2, o_step = G * R * D;  // one split further
+  auto ld = [&](const float* p) { return ld_part<DEV>(p); };
+  float g = -INFINITY;
+  int s = 0;
+  for (; s + 4 <= S; s += 4) {
+    const float m0 = ld(ml + (s + 0) * ml_step), m1 = ld(ml + (s + 1) * ml_step);
+    const float m2 = ld(ml + (s + 2) * ml_step), m3 = ld(ml + (s + 3) * ml_step);
+    g = fmaxf(g, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
+  }
+  for (; s < S; ++s) g = fmaxf(g, ld(ml + s * ml_step));
+  const float g_use = (g == -INFINITY) ? 0.f : g;
+  float lsum = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  s = 0;
+  for (; s + 4 <= S; s += 4) {
+    float m[4], l[4];
+    f32x4 x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m[j] = ld(ml + (s + j) * ml_step);
+      l[j] = ld(ml + (s + j) * ml_step + 1);
+      x[j] = ld_part4<DEV>(po + (s + j) * o_step);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // splits in order, as the one-at-a-time loop
+      const float wgt = fast_exp2(m[j] - g_use);
+      lsum += wgt * l[j];
+      acc += wgt * x[j];
+    }
+  }
+  for (; s < S; ++s) {
+    const float wgt = fast_exp2(ld(ml + s * ml_step) - g_use);
+    lsum += wgt * ld(ml + s * ml_step + 1);
+    acc += wgt * ld_part4<DEV>(po + s * o_step);
+  }
+  const float inv = 1.f / lsum;  // 0/0 -> NaN for a row with no key, as the reference
+  if constexpr (DT == FA2_DTYPE_F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + off) = acc * inv;
+  } else {
+    constexpr bool BF = Elt<DT>::kBF;
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
+        (u32x2){pack2<BF>(acc[0] * inv, acc[1] * inv), pack2<BF>(acc[2] * inv, acc[3] * inv)};
+  }
+}
+
 template <int DT, int D, int MODE>
 __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   const int S = launch_splits(a);
@@ -876,53 +972,59 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
   const int col = (threadIdx.x % kTPR) * 4;
   const int qrow = w.qblk * a.block_rows + r;
   if (r >= a.part_rows || qrow >= w.Lq || col >= a.dv) return;
-  const int64_t G = a.part_slots;
-  const int64_t R = a.part_rows;
-  const float* ml = a.part_ml + (static_cast<int64_t>(blockIdx.x) * R + r) * 2;
-  const float* po = a.part_o + (static_cast<int64_t>(blockIdx.x) * R + r) * D + col;
-  const int64_t ml_step = G * R * 2, o_step = G * R * D;  // one split further
-  float g = -INFINITY;
-  int s = 0;
-  for (; s + 4 <= S; s += 4) {
-    const float m0 = ml[(s + 0) * ml_step], m1 = ml[(s + 1) * ml_step];
-    const float m2 = ml[(s + 2) * ml_step], m3 = ml[(s + 3) * ml_step];
-    g = fmaxf(g, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-  }
-  for (; s < S; ++s) g = fmaxf(g, ml[s * ml_step]);
-  const float g_use = (g == -INFINITY) ? 0.f : g;
-  float lsum = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  s = 0;
-  for (; s + 4 <= S; s += 4) {
-    float m[4], l[4];
-    f32x4 x[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      m[j] = ml[(s + j) * ml_step];
-      l[j] = ml[(s + j) * ml_step + 1];
-      x[j] = *reinterpret_cast<const f32x4*>(po + (s + j) * o_step);
+  combine_row<DT, D>(a, blockIdx.x, r, col, S,
+                     w.o_base + static_cast<int64_t>(qrow) * a.o_ss + col);
+}
+
+// Split merge inside the forward kernel (KArgs::merge_ctr).  The threads that
+// write this unit's partials do so with st_part4<true>; then every thread of
+// the workgroup calls merge_publish (its stores have been performed at
+// device scope) and, after a workgroup barrier, merge_count; `flag` is one
+// LDS word of scratch.  merge_count returns true in every thread of the
+// workgroup whose split completed the unit's count: it then merges
+// (merge_rows, reading the partials at device scope).
+__device__ __forceinline__ void merge_publish() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+__device__ __forceinline__ bool merge_count(const KArgs& a, int unit, int S, int* flag) {
+  if (threadIdx.x == 0) {
+    uint64_t* c = a.merge_ctr + unit;
+    const uint64_t tag = a.merge_tag;
+    uint64_t old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint64_t cnt;
+    for (;;) {
+      cnt = (old >> kMergeCountBits) == tag ? (old & ((uint64_t(1) << kMergeCountBits) - 1)) : 0;
+      const uint64_t nw = (tag << kMergeCountBits) | (cnt + 1);
+      if (__hip_atomic_compare_exchange_strong(c, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))
+        break;
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // splits in order, as the one-at-a-time loop
-      const float wgt = fast_exp2(m[j] - g_use);
-      lsum += wgt * l[j];
-      acc += wgt * x[j];
-    }
+    const bool last = static_cast<int>(cnt) + 1 == S;
+    // the next launch with this tag (a graph replay) starts from zero; no
+    // split of this launch adds to the word after the last one
+    if (last)
+      __hip_atomic_store(c, tag << kMergeCountBits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *static_cast<volatile int*>(flag) = last ? 1 : 0;
   }
-  for (; s < S; ++s) {
-    const float wgt = fast_exp2(ml[s * ml_step] - g_use);
-    lsum += wgt * ml[s * ml_step + 1];
-    acc += wgt * *reinterpret_cast<const f32x4*>(po + s * o_step);
-  }
-  const float inv = 1.f / lsum;  // 0/0 -> NaN for a row with no key, as the reference
-  const int64_t off = w.o_base + static_cast<int64_t>(qrow) * a.o_ss + col;
-  if constexpr (DT == FA2_DTYPE_F32) {
-    *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + off) = acc * inv;
-  } else {
-    constexpr bool BF = Elt<DT>::kBF;
-    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
-        (u32x2){pack2<BF>(acc[0] * inv, acc[1] * inv), pack2<BF>(acc[2] * inv, acc[3] * inv)};
-  }
+  __syncthreads();
+  // (the partials are read after this, at device scope: the count that made
+  // this split the last was taken after every split's stores were performed)
+  return *static_cast<volatile int*>(flag) != 0;
+}
+
+// The merge itself: rows [0, rows) of the unit in part slot `unit`, the
+// output of row r at o_base + (row0 + r) * o_ss; NT threads of the workgroup.
+template <int DT, int D, int NT>
+__device__ __forceinline__ void merge_rows(const KArgs& a, int unit, int S, int rows,
+                                           int64_t o_base, int row0) {
+  constexpr int kTPR = D / 4;
+  constexpr int kRowsPerPass = NT / kTPR;
+  const int col = (threadIdx.x % kTPR) * 4;
+  if (col >= a.dv) return;
+  for (int r = threadIdx.x / kTPR; r < rows; r += kRowsPerPass)
+    combine_row<DT, D, true>(a, unit, r, col, S,
+                             o_base + static_cast<int64_t>(row0 + r) * a.o_ss + col);
 }
 
 // ---------------------------------------------------------------------------

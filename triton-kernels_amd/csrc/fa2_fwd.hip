@@ -14,6 +14,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <random>
 
 #include "fa2_device.h"
 #include "fa2_kernel_lds.h"
@@ -45,6 +46,11 @@
 // (KArgs::claim); 0: the static round walk
 #ifndef FA2_PP_CLAIM
 #define FA2_PP_CLAIM 1
+#endif
+// 1: the decode kernel merges its own splits (KArgs::merge_ctr); 0: a
+// combine launch after it
+#ifndef FA2_DECODE_FOLD
+#define FA2_DECODE_FOLD 1
 #endif
 
 namespace fa2 {
@@ -113,9 +119,10 @@ struct Plan {
   bool plan;        // ragged/paged: the plan kernel orders the work list
   bool dev_splits;  // ... and lowers the automatic split count (KArgs::split_count)
   bool buf;         // paged: every row of the pool has a 31-bit byte offset
+  bool fold;        // splits merged by the forward kernel (KArgs::merge_ctr), no combine
   int64_t max_wgs;  // cap on the persistent grid (0: none)
   uint32_t pool_bytes_k, pool_bytes_v;
-  size_t off_work, off_count, off_ml, off_o, off_cq, off_ck, off_cv, total;
+  size_t off_work, off_count, off_ml, off_o, off_ctr, off_cq, off_ck, off_cv, total;
 };
 
 // K/V tiles are read through buffer descriptors.  Dense and ragged tiles, and
@@ -343,6 +350,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv 
     if (per_split * splits <= cus) pl->plan = false;
   }
   pl->part_rows = kBM;  // the two-head kernel's partial slots assume kBM
+  pl->fold = false;
   return finish_plan(p, pl);
 }
 
@@ -360,6 +368,10 @@ int finish_plan(const fa2_params* p, Plan* pl) {
   pl->off_count = off;  // the item count, the split count, the claim counters at kClaimOffset
   if (p->layout != FA2_LAYOUT_DENSE) off += 256;
   const bool parts = splits > 1 || pl->conv;
+  if (!parts) pl->fold = false;
+  pl->off_ctr = off;  // one merge word per part slot
+  if (pl->fold) off += static_cast<size_t>(pl->grid_x) * sizeof(uint64_t);
+  off = (off + 255) & ~size_t(255);
   pl->off_ml = off;
   if (parts)
     off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * 2 * sizeof(float);
@@ -445,6 +457,9 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   if (pl->plan && (pl->dec || pl->f32) && query_device &&
       pl->grid_x * splits <= cu_count_current_device() * resident)
     pl->plan = false;
+  // The decode kernel merges its own splits: the last split of a unit to
+  // finish combines the unit's partials, so no combine launch follows.
+  pl->fold = FA2_DECODE_FOLD && pl->dec && splits > 1;
   return finish_plan(p, pl);
 }
 
@@ -510,7 +525,7 @@ int launch_typed(KArgs a, const Plan& pl, hipStream_t st) {
   if constexpr (DT != FA2_DTYPE_F32 && (D == 64 || D == 128)) {
     if (pl.dec) {
       FA2_LAUNCH_BUF(fa2_decode_kernel, grid, dim3(kDecThreads));
-      if (pl.splits > 1)
+      if (pl.splits > 1 && !pl.fold)
         hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
                            dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads),
                            0, st, a);
@@ -629,6 +644,20 @@ int workspace_size(const fa2_params* p, size_t* bytes, bool packed) {
 
 // allow_conv = false: fp32 tensors keep the register-staged kernel (no
 // fp16 copies in the workspace; fa2_fwd_noalloc when they do not fit)
+// Tag of one call's merge words (KArgs::merge_tag): a process-wide counter
+// from a random start, skipping the values a cleared or all-ones word holds.
+uint64_t next_merge_tag() {
+  constexpr uint64_t kMask = (uint64_t(1) << kMergeTagBits) - 1;
+  static std::atomic<uint64_t> next{[] {
+    std::random_device rd;
+    return (static_cast<uint64_t>(rd()) << 32) ^ rd();
+  }()};
+  for (;;) {
+    const uint64_t t = next.fetch_add(1, std::memory_order_relaxed) & kMask;
+    if (t != 0 && t != kMask) return t;
+  }
+}
+
 int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) {
   int s = packed ? validate_decode(p) : validate(p);
   if (s != FA2_OK) return s;
@@ -687,6 +716,8 @@ int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) 
   a.part_ml = parts ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
   a.part_o = parts ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
   a.part_rows = pl.part_rows;
+  a.merge_ctr = pl.fold ? reinterpret_cast<uint64_t*>(ws + pl.off_ctr) : nullptr;
+  a.merge_tag = pl.fold ? next_merge_tag() : 0;
   a.pack_m = packed ? static_cast<int32_t>(p->q_len) : 0;
   a.dv = static_cast<int32_t>(p->head_dim);
   a.spin_cap = p->decode_spin_cap > 0 ? p->decode_spin_cap : kDecSpinCap;

@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
   constexpr int L = NS - 1;  // tiles a producer keeps in flight
 
   __shared__ __attribute__((aligned(1024))) char lds[DG::kLdsBytes];
-  __shared__ int counters[2 * NS + 1];  // ready[NS], done[NS], a wait gave up
+  __shared__ int counters[2 * NS + 2];  // ready[NS], done[NS], a wait gave up, merge flag
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -382,39 +382,61 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
       }
   }
   __syncthreads();  // the merge area is reused for the output staging
-  if (!cons || kh != 0) return;
-  if (poisoned) {  // a wait gave up: these rows may have read an unfinished tile
+  // a wait gave up: these rows may have read an unfinished tile
+  auto poison = [&]() {
 #pragma unroll
     for (int d = 0; d < DB; ++d)
 #pragma unroll
       for (int j = 0; j < 16; ++j) o[d][j] = __builtin_nanf("");
     l_sum = 1.f;
-  }
-
-  const int wq_first = q0 + rc * kWaveRows;
+  };
   if (S == 1) {
+    if (!cons || kh != 0) return;
+    if (poisoned) poison();
     const float inv = 1.f / l_sum;  // 0/0 -> NaN for a row with no key, as the reference
     store_o_staged<DT, D>(o, inv, lds + rc * OStage<D>::kBytes, a.o, w.o_base, a.o_ss,
-                          wq_first, w.Lq, lane);
-  } else {
-    // split partials (m, l, unnormalised O), rows the combine reads only
+                          q0 + rc * kWaveRows, w.Lq, lane);
+    return;
+  }
+  if (cons && kh == 0) {
+    if (poisoned) poison();
+    // split partials (m, l, unnormalised O) of the rows that exist
     const int64_t slot_id = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = rc * kWaveRows + l32;
-    if (qrow < w.Lq && r < a.part_rows) {
+    // (read by the merge of this kernel at device scope, or by the combine)
+    auto store = [&](auto dev) {
+      constexpr bool DEV = decltype(dev)::value;
       if (hi == 0) {
         float* ml = a.part_ml + (slot_id * a.part_rows + r) * 2;
-        ml[0] = m_all;
-        ml[1] = l_sum;
+        if constexpr (DEV) {
+          st_dev(ml, m_all);
+          st_dev(ml + 1, l_sum);
+        } else {
+          ml[0] = m_all;
+          ml[1] = l_sum;
+        }
       }
       float* pout = a.part_o + (slot_id * a.part_rows + r) * D + hi * 4;
 #pragma unroll
       for (int d = 0; d < DB; ++d)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4*>(pout + d * 32 + g * 8) =
-              (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
+          st_part4<DEV>(pout + d * 32 + g * 8, (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1],
+                                                       o[d][g * 4 + 2], o[d][g * 4 + 3]});
+    };
+    if (qrow < w.Lq && r < a.part_rows) {
+      if (a.merge_ctr)
+        store(std::true_type{});
+      else
+        store(std::false_type{});
     }
   }
+  if (!a.merge_ctr) return;  // the combine kernel merges
+  // the split that completes the unit's count merges its partials
+  merge_publish();
+  __syncthreads();
+  if (!merge_count(a, blockIdx.x, S, counters + 2 * NS + 1)) return;
+  merge_rows<DT, D, kDecThreads>(a, blockIdx.x, S, min(a.part_rows, w.Lq - q0), w.o_base, q0);
 }
 
 }  // namespace fa2

@@ -106,7 +106,7 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
             q_strides, o_strides, qi=None, kvi=None, kt=None, vt=None,
             page_size=None, max_workgroups: int = 0, kv_len_max: int = 0,
             noalloc: bool = False, arith: int = 0, decode_spin_cap: int = 0,
-            kernel: int = 0) -> None:
+            kernel: int = 0, workspace: torch.Tensor | None = None) -> None:
     """Fill ``fa2_params`` and enqueue ``fa2_fwd`` (``decode=False``) or
     ``fa2_decode_fwd`` on torch's current stream of ``q``'s device.
 
@@ -117,7 +117,9 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
     ``max_workgroups`` the cap on the persistent grid (0 = none), ``arith`` the
     fa2_arith of fp32 tensors (``_fa2.ARITH_FP32``: fp32 throughout),
     ``decode_spin_cap`` the decode kernel's wait bound (tests only), ``kernel``
-    the fa2_kernel choice of the forward kernel (``_fa2.KERNEL_AUTO``...).  ``noalloc``
+    the fa2_kernel choice of the forward kernel (``_fa2.KERNEL_AUTO``...), ``workspace``
+    a caller's uint8 device buffer of at least the workspace size to use instead of
+    an allocation (tests).  ``noalloc``
     enqueues ``fa2_fwd_noalloc`` instead (no workspace; prefill only).  Everything but
     the pointers depends only on the call signature, so that part of the
     parameter block (and its workspace size) is built once per signature.
@@ -178,7 +180,12 @@ def enqueue(*, decode: bool, layout: int, mask: int, num_splits: int, batch: int
             return
         ws = None
         if ws_bytes:
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            if workspace is not None:
+                if workspace.numel() < ws_bytes or workspace.device != dev:
+                    raise ValueError(f"workspace needs {ws_bytes} bytes on {dev}")
+                ws = workspace
+            else:
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
         _fa2.forward(p, handle, decode)
         if ws is not None:

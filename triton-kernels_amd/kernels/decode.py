@@ -86,13 +86,14 @@ def decode_attention(
 
 def _run_decode(name, q4, k, v, out4, *, layout, causal, batch, q_heads, kv_heads, head_dim,
                 kv_indptr, k_block_table, v_block_table, kv_page_size, num_splits=0,
-                decode_spin_cap=0):
+                decode_spin_cap=0, workspace=None):
     """Shared by decode_attention and speculative_decode_attention.
 
     ``q4`` / ``out4`` are ``[B, QH, M, D]`` views; ``out4`` must be a view
     of the caller's output so the kernels write it in place.
     ``decode_spin_cap`` (tests only, fa2_params.decode_spin_cap) bounds the
-    decode kernel's ring waits; 0 = the library's bound."""
+    decode kernel's ring waits; 0 = the library's bound.  ``workspace``
+    (tests only) is a uint8 device buffer used instead of an allocation."""
     check_dtype_and_dim(name, q4.dtype, head_dim)
     if q_heads % kv_heads != 0:
         raise ValueError(f"{name}: q_heads ({q_heads}) must be a multiple of kv_heads "
@@ -148,6 +149,6 @@ def _run_decode(name, q4, k, v, out4, *, layout, causal, batch, q_heads, kv_head
             q=q4, k=k, v=v, out=dst, q_strides=abi_strides(q4), o_strides=abi_strides(dst),
             kvi=kvi, kt=kt, vt=vt, page_size=kv_page_size,
             kv_len_max=kt.shape[1] * kv_page_size if kt is not None else 0,
-            decode_spin_cap=decode_spin_cap)
+            decode_spin_cap=decode_spin_cap, workspace=workspace)
     if dst is not out4:
         out4.copy_(dst)
