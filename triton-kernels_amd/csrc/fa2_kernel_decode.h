@@ -27,9 +27,15 @@
 // between reads, and every poll gives up after KArgs::spin_cap reads
 // (kDecSpinCap unless a test lowers it), so a wave cannot wait forever even
 // if a counter were wrong.  A workgroup in which any wait gave up writes NaN
-// for all its rows (output or split partials, which the combine turns into
+// for all its rows (output or split partials, which the merge turns into
 // NaN rows) and adds 1 to g_decode_giveups, which fa2_decode_wait_giveups()
 // reads: a wrong result is never silent.
+//
+// With several splits the kernel merges them itself (KArgs::merge_ctr): each
+// split writes its partials at device scope and counts itself in the unit's
+// merge word; the split that completes the count combines all partials with
+// the combine kernel's arithmetic (combine_row), so the output is the same
+// bit for bit and no combine launch follows.
 #pragma once
 
 #include "fa2_kernel_lds.h"
