@@ -6,7 +6,10 @@ all sequences; for paged K/V it knows the block table's width.  The plan
 kernel knows the longest sweep of the call and lowers the count
 (csrc/fa2_device.h, fa2_plan_kernel): the forward kernels run that many
 splits out of a grid sized for the host's count, and the combine kernel
-exits at once when one split remains.  Each split count gives the same
+exits at once when one split remains.  (A ragged launch whose workgroups
+all fit on the GPU at once skips the plan kernel: each workgroup derives
+the same split count itself, and the forward kernel merges the splits.)
+Each split count gives the same
 arithmetic wherever it is decided, so an automatic call must equal, bit for
 bit, the call that forces the count the plan kernel chose.  It must also
 pass the oracle bars.
@@ -115,3 +118,26 @@ def test_long_sequence_keeps_host_splits():
     eight, _ = run(case, "ragged", False, 8)
     assert same(auto, eight)
     check_all(case, "ragged", False, unpack(case, "ragged", auto, kw))
+
+
+@pytest.mark.parametrize("heads", [(8, 2), (8, 8)], ids=["gqa", "mha"])
+@pytest.mark.parametrize("causal,splits", [(False, 0), (False, 1), (False, 3), (True, 0),
+                                           (True, 2)])
+def test_inline_plan_equals_plan_kernel(heads, causal, splits):
+    """A ragged launch whose workgroups all fit on the GPU at once runs
+    without the plan kernel: each workgroup derives the item list and the
+    split count from the sequence lengths, and the forward kernel merges its
+    own splits (no combine launch).  max_workgroups > 0 keeps the plan
+    kernel and the combine kernel.  Both must give the same output bit for
+    bit (each unit's arithmetic does not depend on where it runs), and pass
+    the oracle bars."""
+    QH, KVH = heads
+    lens = [64, 200, 1, 130, 17, 300]
+    kv = lens if causal else [300, 900, 50, 1200, 10, 640]
+    case = make_case(len(lens), QH, KVH, 128, "self" if causal else "cross", torch.bfloat16,
+                     "ragged", 5400 + QH + 10 * int(causal) + splits, q_lens=lens, kv_lens=kv)
+    print(f"inline plan {QH}/{KVH} causal={causal} splits={splits}", flush=True)
+    inline, kw = run(case, "ragged", causal, splits)
+    planned, _ = run(case, "ragged", causal, splits, max_workgroups=1 << 20)
+    assert same(inline, planned)
+    check_all(case, "ragged", causal, unpack(case, "ragged", inline, kw))

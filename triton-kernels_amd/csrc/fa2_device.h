@@ -145,6 +145,12 @@ struct KArgs {
   // from zero as well.  null: partials go to the combine kernel.
   uint64_t* merge_ctr;
   uint64_t merge_tag;  // nonzero, < 2^kMergeTagBits - 1, distinct per call
+  // Ragged launch without a plan kernel, all of whose workgroups are
+  // resident at once: each workgroup derives the item list (InlinePlan) and,
+  // with automatic splits (auto_splits), the split count from the sequence
+  // lengths itself.
+  int32_t inline_plan;
+  int32_t auto_splits;
 };
 
 constexpr int kMergeCountBits = 24;
@@ -314,6 +320,20 @@ struct Work {
   int off;                 // causal diagonal offset: key j visible iff j <= i + off
 };
 
+// Item list of a ragged launch without a plan kernel (KArgs::inline_plan),
+// built in LDS by every workgroup (build_inline_plan): item i is q-block (or
+// q-block pair) i - cum[b] of the sequence b with cum[b] <= i < cum[b + 1],
+// sequence by sequence; every workgroup of such a launch is resident at once,
+// so the order of the items does not matter.
+constexpr int kInlinePlanMaxBatch = 256;
+struct InlinePlan {
+  int cum[kInlinePlanMaxBatch + 1];
+  int qi[kInlinePlanMaxBatch + 1];  // copies of q_indptr and kv_indptr
+  int ki[kInlinePlanMaxBatch + 1];
+  int max_cost;  // KV tiles of the heaviest item
+  int splits;    // the launch's split count
+};
+
 // Workgroup ids are dispatched round-robin over the 8 XCDs (each with its own
 // L2).  Ids are laid out as ((blk * G + g) * 8 + p): the 8 (item, kv head)
 // pairs of block `blk` go to 8 different XCDs, and the G query heads that
@@ -323,8 +343,12 @@ constexpr int kXcds = 8;
 
 // A unit may cover `heads` consecutive query heads of one kv group (the
 // ping-pong kernel takes two); w.h is then the first of them.
-template <int MODE>
-__device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1) {
+// ip: the inline plan's table (null: none); UNI: its reads pass through
+// readfirstlane (they are wave-uniform), so that a kernel that derives loop
+// bounds from the result keeps them in scalar registers.
+template <int MODE, bool UNI = false>
+__device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1,
+                                            const InlinePlan* ip = nullptr) {
   Work w;
   w.valid = true;
   const int group = a.hq / a.hkv;
@@ -361,6 +385,19 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1
         return w;
       }
       it = a.work[item];
+    } else if (MODE == FA2_LAYOUT_RAGGED && ip) {
+      auto rd = [](const int& x) { return UNI ? __builtin_amdgcn_readfirstlane(x) : x; };
+      if (item >= rd(ip->cum[a.batch])) {
+        w.valid = false;
+        return w;
+      }
+      int lo = 0, hi = a.batch;  // the last b with cum[b] <= item
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (rd(ip->cum[mid]) <= item) lo = mid;
+        else hi = mid;
+      }
+      it = make_int2(lo, item - rd(ip->cum[lo]));
     } else {
       // no plan (uniform q-block count, every workgroup resident at once, so
       // the order does not matter): items in (q-block, sequence) order
@@ -373,15 +410,17 @@ __device__ __forceinline__ Work decode_work(const KArgs& a, int L, int heads = 1
     w.b = it.x;
     w.qblk = it.y;
     if constexpr (MODE == FA2_LAYOUT_RAGGED) {
-      const int ks = a.kv_indptr[w.b];
-      w.Lk = a.kv_indptr[w.b + 1] - ks;
+      // (the offsets from the inline plan's copies in LDS when there is one)
+      auto rd = [](const int& x) { return UNI ? __builtin_amdgcn_readfirstlane(x) : x; };
+      const int ks = ip ? rd(ip->ki[w.b]) : a.kv_indptr[w.b];
+      w.Lk = (ip ? rd(ip->ki[w.b + 1]) : a.kv_indptr[w.b + 1]) - ks;
       if (a.pack_m > 0) {  // decode: dense q/o over a ragged K/V
         w.Lq = a.q_len;
         w.q_base = w.b * a.q_sb + w.h * a.q_sh;
         w.o_base = w.b * a.o_sb + w.h * a.o_sh;
       } else {
-        const int qs = a.q_indptr[w.b];
-        w.Lq = a.q_indptr[w.b + 1] - qs;
+        const int qs = ip ? rd(ip->qi[w.b]) : a.q_indptr[w.b];
+        w.Lq = (ip ? rd(ip->qi[w.b + 1]) : a.q_indptr[w.b + 1]) - qs;
         w.q_base = qs * a.q_ss + w.h * a.q_sh;
         w.o_base = qs * a.o_ss + w.h * a.o_sh;
       }
@@ -919,37 +958,49 @@ __device__ __forceinline__ void combine_row(const KArgs& a, int unit, int r, int
   const int64_t ml_step = G * R * 2, o_step = G * R * D;  // one split further
   auto ld = [&](const float* p) { return ld_part<DEV>(p); };
   float g = -INFINITY;
-  int s = 0;
-  for (; s + 4 <= S; s += 4) {
-    const float m0 = ld(ml + (s + 0) * ml_step), m1 = ld(ml + (s + 1) * ml_step);
-    const float m2 = ld(ml + (s + 2) * ml_step), m3 = ld(ml + (s + 3) * ml_step);
-    g = fmaxf(g, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-  }
-  for (; s < S; ++s) g = fmaxf(g, ld(ml + s * ml_step));
-  const float g_use = (g == -INFINITY) ? 0.f : g;
   float lsum = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  s = 0;
-  for (; s + 4 <= S; s += 4) {
-    float m[4], l[4];
-    f32x4 x[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      m[j] = ld(ml + (s + j) * ml_step);
-      l[j] = ld(ml + (s + j) * ml_step + 1);
-      x[j] = ld_part4<DEV>(po + (s + j) * o_step);
+  if constexpr (DEV) {
+    // (the merge inside a forward kernel: one split at a time, the same
+    // operations in the same order as the loops below, in less code)
+    for (int s = 0; s < S; ++s) g = fmaxf(g, ld(ml + s * ml_step));
+    const float g_use = (g == -INFINITY) ? 0.f : g;
+    for (int s = 0; s < S; ++s) {
+      const float wgt = fast_exp2(ld(ml + s * ml_step) - g_use);
+      lsum += wgt * ld(ml + s * ml_step + 1);
+      acc += wgt * ld_part4<DEV>(po + s * o_step);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // splits in order, as the one-at-a-time loop
-      const float wgt = fast_exp2(m[j] - g_use);
-      lsum += wgt * l[j];
-      acc += wgt * x[j];
+  } else {
+    int s = 0;
+    for (; s + 4 <= S; s += 4) {
+      const float m0 = ld(ml + (s + 0) * ml_step), m1 = ld(ml + (s + 1) * ml_step);
+      const float m2 = ld(ml + (s + 2) * ml_step), m3 = ld(ml + (s + 3) * ml_step);
+      g = fmaxf(g, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
     }
-  }
-  for (; s < S; ++s) {
-    const float wgt = fast_exp2(ld(ml + s * ml_step) - g_use);
-    lsum += wgt * ld(ml + s * ml_step + 1);
-    acc += wgt * ld_part4<DEV>(po + s * o_step);
+    for (; s < S; ++s) g = fmaxf(g, ld(ml + s * ml_step));
+    const float g_use = (g == -INFINITY) ? 0.f : g;
+    s = 0;
+    for (; s + 4 <= S; s += 4) {
+      float m[4], l[4];
+      f32x4 x[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        m[j] = ld(ml + (s + j) * ml_step);
+        l[j] = ld(ml + (s + j) * ml_step + 1);
+        x[j] = ld_part4<DEV>(po + (s + j) * o_step);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {  // splits in order, as the one-at-a-time loop
+        const float wgt = fast_exp2(m[j] - g_use);
+        lsum += wgt * l[j];
+        acc += wgt * x[j];
+      }
+    }
+    for (; s < S; ++s) {
+      const float wgt = fast_exp2(ld(ml + s * ml_step) - g_use);
+      lsum += wgt * ld(ml + s * ml_step + 1);
+      acc += wgt * ld_part4<DEV>(po + s * o_step);
+    }
   }
   const float inv = 1.f / lsum;  // 0/0 -> NaN for a row with no key, as the reference
   if constexpr (DT == FA2_DTYPE_F32) {
@@ -1013,6 +1064,31 @@ __device__ __forceinline__ bool merge_count(const KArgs& a, int unit, int S, int
   return *static_cast<volatile int*>(flag) != 0;
 }
 
+// Split partials of one row (this lane's half: hi), the O^T accumulator
+// layout of the 16-bit kernels (row l32, dims 32d + 8g + 4hi + j at
+// o[d][4g + j]), into part slot `slot` (split * part_slots + unit).
+template <bool DEV, int D>
+__device__ __forceinline__ void store_partial_rows(const KArgs& a, int64_t slot, int r, int hi,
+                                                   float m, float l, const f32x16 (&o)[D / 32]) {
+  if (hi == 0) {
+    float* ml = a.part_ml + (slot * a.part_rows + r) * 2;
+    if constexpr (DEV) {
+      st_dev(ml, m);
+      st_dev(ml + 1, l);
+    } else {
+      ml[0] = m;
+      ml[1] = l;
+    }
+  }
+  float* po = a.part_o + (slot * a.part_rows + r) * D + hi * 4;
+#pragma unroll
+  for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      st_part4<DEV>(po + d * 32 + g * 8,
+                    (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]});
+}
+
 // The merge itself: rows [0, rows) of the unit in part slot `unit`, the
 // output of row r at o_base + (row0 + r) * o_ss; NT threads of the workgroup.
 template <int DT, int D, int NT>
@@ -1061,6 +1137,71 @@ __device__ __forceinline__ int plan_items(const KArgs& a, int nq) {
 }
 __device__ __forceinline__ int plan_cost_block(const KArgs& a, int j, int nq) {
   return a.qpair ? min(2 * j + 1, nq - 1) : j;
+}
+
+// The item list and split count of a launch without a plan kernel
+// (KArgs::inline_plan, batch <= kInlinePlanMaxBatch), called by all threads
+// of the workgroup: the first wave writes the sequence offsets, the items of
+// each sequence as the plan kernel counts them, their prefix sums and the
+// plan kernel's split count (the host's heuristic with the longest KV sweep
+// in place of its bound), then one barrier.
+template <int MODE>
+__device__ __forceinline__ void build_inline_plan(const KArgs& a, InlinePlan* ip) {
+  static_assert(MODE == FA2_LAYOUT_RAGGED, "ragged launches only");
+  // the first wave alone (kPer sequences per lane), one barrier for all
+  constexpr int kPer = (kInlinePlanMaxBatch + 63) / 64;
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    int qs[kPer + 1], ks[kPer + 1];
+#pragma unroll
+    for (int j = 0; j <= kPer; ++j) {
+      const int t = min(tid * kPer + j, a.batch);
+      qs[j] = a.q_indptr[t];
+      ks[j] = a.kv_indptr[t];
+    }
+    int ni[kPer], sum = 0, cost = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int b = tid * kPer + j;
+      const int Lq = max(qs[j + 1] - qs[j], 0);  // as seq_lens
+      const int Lk = max(ks[j + 1] - ks[j], 0);
+      const int nq = (Lq + a.block_rows - 1) / a.block_rows;
+      ni[j] = b < a.batch ? plan_items(a, nq) : 0;
+      if (ni[j] > 0)
+        cost = max(cost, block_cost(a.mask, plan_cost_block(a, ni[j] - 1, nq), Lq, Lk,
+                                    a.pack_m > 0));
+      sum += ni[j];
+      if (b <= a.batch) {
+        ip->qi[b] = qs[j];
+        ip->ki[b] = ks[j];
+      }
+    }
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d);
+      if (tid >= d) incl += y;
+      cost = max(cost, __shfl_xor(cost, d));
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int b = tid * kPer + j;
+      run += ni[j];
+      if (b < a.batch) ip->cum[b + 1] = run;
+    }
+    if (tid == 0) {
+      ip->cum[0] = 0;
+      ip->max_cost = cost;
+      const int s = cost / kMinSplitTiles;
+      ip->splits = !a.auto_splits ? a.num_splits : (s < 1 ? 1 : (s < a.num_splits ? s : a.num_splits));
+    }
+    if (tid == 63 && a.batch == 64 * kPer) {  // the end offsets of a full table
+      ip->qi[a.batch] = qs[kPer];
+      ip->ki[a.batch] = ks[kPer];
+    }
+  }
+  __syncthreads();
 }
 
 // fp32 -> fp16 copies of q, k and v, rounded as the 16-bit kernels round

@@ -52,6 +52,11 @@
 #ifndef FA2_DECODE_FOLD
 #define FA2_DECODE_FOLD 1
 #endif
+// 1: ragged launches that fit the GPU at once run without the plan kernel
+// and merge their own splits (see make_plan); 0: plan and combine launches
+#ifndef FA2_INLINE_PLAN
+#define FA2_INLINE_PLAN 1
+#endif
 
 namespace fa2 {
 namespace {
@@ -120,6 +125,7 @@ struct Plan {
   bool dev_splits;  // ... and lowers the automatic split count (KArgs::split_count)
   bool buf;         // paged: every row of the pool has a 31-bit byte offset
   bool fold;        // splits merged by the forward kernel (KArgs::merge_ctr), no combine
+  bool inline_plan; // ragged without the plan kernel (KArgs::inline_plan)
   int64_t max_wgs;  // cap on the persistent grid (0: none)
   uint32_t pool_bytes_k, pool_bytes_v;
   size_t off_work, off_count, off_ml, off_o, off_ctr, off_cq, off_ck, off_cv, total;
@@ -351,6 +357,26 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv 
   }
   pl->part_rows = kBM;  // the two-head kernel's partial slots assume kBM
   pl->fold = false;
+  // A ragged launch whose workgroups are all resident at once needs no list
+  // either: every workgroup of the two-head or the one-head kernel derives
+  // the items (and the split count the plan kernel would derive) from the
+  // sequence lengths itself, and the order of the items does not matter.
+  // With several splits the forward kernel then merges them itself, so
+  // neither the plan nor the combine kernel is launched.
+  pl->inline_plan = false;
+  const bool lds_dim = p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
+  if (FA2_INLINE_PLAN && p->layout == FA2_LAYOUT_RAGGED && half && !pl->conv && !pl->f32 &&
+      !pl->shortk && lds_dim && p->batch <= kInlinePlanMaxBatch && p->max_workgroups == 0) {
+    const int64_t cus = query_device ? cu_count_current_device() : 256;
+    const int64_t resident = pl->pp ? 1 : (p->head_dim > 128 ? 1 : FA2_LDS_OCCUPANCY);
+    const int64_t per_split = pl->pp ? pl->grid_pp : pl->grid_x;
+    if (per_split * splits <= cus * resident) {
+      pl->inline_plan = true;
+      pl->plan = false;
+      pl->dev_splits = false;
+      pl->fold = splits > 1;
+    }
+  }
   return finish_plan(p, pl);
 }
 
@@ -460,6 +486,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   // The decode kernel merges its own splits: the last split of a unit to
   // finish combines the unit's partials, so no combine launch follows.
   pl->fold = FA2_DECODE_FOLD && pl->dec && splits > 1;
+  pl->inline_plan = false;
   return finish_plan(p, pl);
 }
 
@@ -549,6 +576,9 @@ int launch_typed(KArgs a, const Plan& pl, hipStream_t st) {
             if (a.claim)
               hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, MODE, true, true>), gpp,
                                  dim3(kPPThreads), 0, st, a);
+            else if (MODE == FA2_LAYOUT_RAGGED && a.inline_plan)
+              hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, FA2_LAYOUT_RAGGED, true, false, true>),
+                                 gpp, dim3(kPPThreads), 0, st, a);
             else
               FA2_LAUNCH_BUF(fa2_fwd_pp_kernel, gpp, dim3(kPPThreads));
           } else {
@@ -565,7 +595,7 @@ int launch_typed(KArgs a, const Plan& pl, hipStream_t st) {
   if (a.part_out) {  // fp32 output of fp16 copies (Plan::conv)
     hipLaunchKernelGGL((fa2_combine_kernel<FA2_DTYPE_F32, D, MODE>), cgrid, dim3(kThreads), 0, st,
                        a);
-  } else if (pl.splits > 1) {
+  } else if (pl.splits > 1 && !pl.fold) {
     hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>), cgrid, dim3(kThreads), 0, st, a);
   }
   return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
@@ -718,6 +748,8 @@ int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) 
   a.part_rows = pl.part_rows;
   a.merge_ctr = pl.fold ? reinterpret_cast<uint64_t*>(ws + pl.off_ctr) : nullptr;
   a.merge_tag = pl.fold ? next_merge_tag() : 0;
+  a.inline_plan = pl.inline_plan ? 1 : 0;
+  a.auto_splits = p->num_splits == 0 ? 1 : 0;
   a.pack_m = packed ? static_cast<int32_t>(p->q_len) : 0;
   a.dv = static_cast<int32_t>(p->head_dim);
   a.spin_cap = p->decode_spin_cap > 0 ? p->decode_spin_cap : kDecSpinCap;

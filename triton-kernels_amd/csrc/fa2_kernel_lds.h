@@ -529,11 +529,20 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : FA2_LDS_OCCUPANCY) void fa2
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  const Work w = decode_work<MODE>(a, blockIdx.x);
+  // a ragged launch without a plan kernel: the item list in LDS
+  const InlinePlan* ip = nullptr;
+  if constexpr (MODE == FA2_LAYOUT_RAGGED) {
+    __shared__ InlinePlan iplan;
+    if (a.inline_plan) {
+      build_inline_plan<MODE>(a, &iplan);
+      ip = &iplan;
+    }
+  }
+  const Work w = decode_work<MODE>(a, blockIdx.x, 1, ip);
   if (!w.valid) return;
   const int q0 = w.qblk * kBM;
   const int split = blockIdx.y;
-  const int S = launch_splits(a);
+  const int S = ip ? ip->splits : launch_splits(a);
   if (split >= S) return;
 
   const int kv_end = kv_end_for_unit(a, q0, w.Lq, w.Lk, w.off);
@@ -771,22 +780,23 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : FA2_LDS_OCCUPANCY) void fa2
     store_o_staged<DT, D>(o, inv, lds + wave * OStage<D>::kBytes, a.o, w.o_base, a.o_ss,
                           wq_first, w.Lq, lane);
   } else {
-    // only rows the combine reads (r < part_rows, q0 + r < Lq) are written
+    // only rows the merge reads (r < part_rows, q0 + r < Lq) are written
     const int64_t slot = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = wave * kWaveRows + l32;
     if (qrow < w.Lq && r < a.part_rows) {
-      if (hi == 0) {
-        float* ml = a.part_ml + (slot * a.part_rows + r) * 2;
-        ml[0] = m_run;
-        ml[1] = l_tot;
-      }
-      float* po = a.part_o + (slot * a.part_rows + r) * D + hi * 4;
-#pragma unroll
-      for (int d = 0; d < DB; ++d)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
-              (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
+      if (MODE == FA2_LAYOUT_RAGGED && a.merge_ctr)
+        store_partial_rows<true, D>(a, slot, r, hi, m_run, l_tot, o);
+      else
+        store_partial_rows<false, D>(a, slot, r, hi, m_run, l_tot, o);
+    }
+    // (only ragged launches merge here: KArgs::inline_plan)
+    if (MODE == FA2_LAYOUT_RAGGED && a.merge_ctr) {  // the split that completes the count merges
+      __shared__ int merge_flag;
+      merge_publish();
+      __syncthreads();
+      if (merge_count(a, blockIdx.x, S, &merge_flag))
+        merge_rows<DT, D, kThreads>(a, blockIdx.x, S, min(a.part_rows, w.Lq - q0), w.o_base,
+                                    q0);
     }
   }
 }

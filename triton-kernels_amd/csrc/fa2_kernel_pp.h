@@ -118,9 +118,13 @@ struct PPUnit {
 
 // CLAIM: the unit walk by claims (KArgs::claim, ragged/paged only), a
 // separate instantiation so that the static walk keeps its registers.
-template <int DT, int D, int MODE, bool BUF, bool CLAIM = false>
+// INLINE: a ragged launch without a plan kernel (KArgs::inline_plan): the
+// item list from build_inline_plan, and the splits merged here; a separate
+// instantiation for the same reason.
+template <int DT, int D, int MODE, bool BUF, bool CLAIM = false, bool INLINE = false>
 __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   static_assert(DT != FA2_DTYPE_F32, "fp32 uses the register-staged kernel");
+  static_assert(!INLINE || (MODE == FA2_LAYOUT_RAGGED && !CLAIM), "inline plans: ragged, static walk");
   constexpr bool BF = Elt<DT>::kBF;
   constexpr int DC = D / 16;  // MFMA k-steps of S (16 head dims each)
   constexpr int DB = D / 32;  // 32-dim blocks of O^T
@@ -147,7 +151,14 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   const int hi = lane >> 5;
   const int group = a.hq / a.hkv;
   const int split = blockIdx.y;
-  const int S = launch_splits(a);
+  // a ragged launch without a plan kernel: the item list in LDS
+  const InlinePlan* ip = nullptr;
+  if constexpr (INLINE) {
+    __shared__ InlinePlan iplan;
+    build_inline_plan<MODE>(a, &iplan);
+    ip = &iplan;
+  }
+  const int S = INLINE ? __builtin_amdgcn_readfirstlane(ip->splits) : launch_splits(a);
   if (split >= S) return;
   const bool causal = a.mask != FA2_MASK_NONE;
   char* const stage = lds + kSlotBytes + wave * OStage<kStageDims>::kBytes;
@@ -175,7 +186,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
     return r * P + pos;
   };
   auto make_unit = [&](int L, PPUnit& u) -> bool {
-    u.w = decode_work<MODE>(a, L, 2);
+    u.w = decode_work<MODE, true>(a, L, 2, ip);
     if (!u.w.valid) return false;
     int kv_end;
     if (a.qpair) {  // MHA: q-blocks 2k (group 0) and 2k + 1 (group 1) of one head
@@ -590,18 +601,26 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
             ((w.pair / kXcds) * group + w.hg + grp) * kXcds + w.pair % kXcds;
         const int64_t slot = static_cast<int64_t>(split) * a.part_slots + unit;
         const int rr = wq * kWaveRows + l32;
-        if (hi == 0) {
-          float* ml = a.part_ml + (slot * a.part_rows + rr) * 2;
-          ml[0] = m_run;
-          ml[1] = l_tot;
-        }
-        float* po = a.part_o + (slot * a.part_rows + rr) * D + hi * 4;
-#pragma unroll
-        for (int d = 0; d < DB; ++d)
-#pragma unroll
-          for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
-                (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
+        if (INLINE && a.merge_ctr)
+          store_partial_rows<true, D>(a, slot, rr, hi, m_run, l_tot, o);
+        else
+          store_partial_rows<false, D>(a, slot, rr, hi, m_run, l_tot, o);
+      }
+    }
+    // Splits merged in this kernel: the split that completes the unit's
+    // count (kept in the first head's part slot) merges both heads.  Both
+    // groups pass the same two barriers, so their pairing is unchanged.
+    if (INLINE && S > 1 && a.merge_ctr) {
+      __shared__ int merge_flag;
+      merge_publish();
+      __syncthreads();
+      const int unit0 = ((w.pair / kXcds) * group + w.hg) * kXcds + w.pair % kXcds;
+      if (merge_count(a, unit0, S, &merge_flag)) {
+        const int q0 = w.qblk * kBM;
+        const int rows = min(kBM, w.Lq - q0);
+        merge_rows<DT, D, kPPThreads>(a, unit0, S, rows, w.o_base, q0);
+        if (w.hg + 1 < group)
+          merge_rows<DT, D, kPPThreads>(a, unit0 + kXcds, S, rows, w.o_base + a.o_sh, q0);
       }
     }
 
