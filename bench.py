@@ -20,8 +20,11 @@ resident in HBM.  Prints ONE JSON line (rank 0, N=1):
 
   python bench.py [--steps K] [--warmup W] [--config c2] [--dtype bf16]
                   [--no-cpu] [--flush] [--windows 5]
-  python bench.py --sweep [--sweep-out FILE]   # the reference benchmark's
-                  shapes (benchmarks/attention.py), one table row per point
+  python bench.py --sweep [--sweep-out FILE] [--sweep-only TERMS]   # the
+                  reference benchmark's shapes (benchmarks/attention.py), one
+                  table row per point
+  python bench.py --config c1 --host-cost 2000   # host us per call
+  python bench.py --config c1 --graph 200        # HIP-graph replays vs eager
 
 ``--gpus N`` with N > 1 exits: this build measures one GPU.
 """
@@ -212,6 +215,79 @@ def sweep(args) -> int:
     return 0
 
 
+def host_cost(args, w, step, stream) -> int:
+    """Host microseconds per call of N back-to-back calls (the time the
+    Python wrapper and the launch take before the loop can issue the next
+    call; the GPU keeps running the queued kernels), through the launch
+    extension and through the ctypes path of flash_attention_v2 (the same
+    entry point and parameter block), with the GPU time per call of each."""
+    from kernels import attention
+
+    n = args.host_cost
+    res = {}
+    paths = [("extension", True), ("ctypes", False)] if w.kind == "prefill" else [("ctypes", None)]
+    for name, use_ext in paths:
+        prev = attention.USE_EXT
+        if use_ext is not None:
+            attention.USE_EXT = use_ext
+        try:
+            for _ in range(args.warmup):
+                step()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            t0 = time.perf_counter()
+            for _ in range(n):
+                step()
+            t1 = time.perf_counter()
+            b.record(stream)
+            torch.cuda.synchronize()
+        finally:
+            attention.USE_EXT = prev
+        res[name] = {"host_us_per_call": round((t1 - t0) * 1e6 / n, 2),
+                     "gpu_us_per_call": round(a.elapsed_time(b) * 1e3 / n, 2)}
+    print(json.dumps({"mode": "host_cost", "config": DESCR[args.config],
+                      "dtype": DTYPE_NAME[w.dtype], "calls": n, "paths": res}))
+    return 0
+
+
+def graph_replay(args, w, step, stream) -> int:
+    """GPU microseconds per call of N replays of one captured step (HIP graph:
+    no host cost per call) and of N eager back-to-back calls, one event pair
+    around each run; replays are checked against an eager call bit for bit."""
+    n = args.graph
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = step()
+
+    def run(fn):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(n):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / n
+
+    run(g.replay)
+    replay_us = run(g.replay)
+    eager_us = run(step)
+    same = bool(torch.equal(out, step()))
+    print(json.dumps({"mode": "graph_replay", "config": DESCR[args.config],
+                      "dtype": DTYPE_NAME[w.dtype], "calls": n,
+                      "graph_us_per_call": round(replay_us, 2),
+                      "eager_us_per_call": round(eager_us, 2),
+                      "replay_equals_eager": same}))
+    return 0 if same else 1
+
+
 def hbm_traffic(config: str, dtype: str):
     """HBM bytes per launch of the workload's forward kernel, from the
     committed counter summary (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE,
@@ -256,6 +332,12 @@ def main(argv=None):
     ap.add_argument("--sweep-only", default=None, metavar="TERMS",
                     help="comma-separated terms (e.g. 'ragged,bf16,q128,kv128'): run only the "
                          "sweep points whose description holds every term")
+    ap.add_argument("--host-cost", type=int, default=0, metavar="N",
+                    help="only time the host side of N back-to-back calls of the config's "
+                         "step (launch extension and ctypes paths), with their GPU time")
+    ap.add_argument("--graph", type=int, default=0, metavar="N",
+                    help="only time N replays of one captured step (HIP graph) against N "
+                         "eager calls, GPU time per call")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "the FETCH_SIZE / WRITE_SIZE counters against known bytes")
@@ -361,6 +443,10 @@ def main(argv=None):
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
+    if args.host_cost:
+        return host_cost(args, w, step, stream)
+    if args.graph:
+        return graph_replay(args, w, step, stream)
     if flush_buf is None:
         # back-to-back steps; one event pair per window on the kernels' stream
         wall, win = time_steps(step, args.steps, args.windows, stream)

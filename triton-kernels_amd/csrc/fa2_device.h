@@ -916,39 +916,14 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : 2) void fa2_fwd_kernel(KArg
 template <int D>
 constexpr int kCombineRows = kThreads / (D / 4);  // rows per workgroup
 
-// Partials of a merge inside the forward kernel are written and read at
-// device scope (relaxed agent-scope atomics: `sc1` loads and stores, coherent
-// across the XCDs' L2 caches without the cache-wide writeback and invalidate
-// of a release/acquire fence); the combine kernel reads them plainly.
-__device__ __forceinline__ float ld_dev(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(float* p, float x) {
-  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <bool DEV>
-__device__ __forceinline__ float ld_part(const float* p) {
-  if constexpr (DEV) return ld_dev(p);
-  else return *p;
-}
-template <bool DEV>
-__device__ __forceinline__ f32x4 ld_part4(const float* p) {
-  if constexpr (DEV) return (f32x4){ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3)};
-  else return *reinterpret_cast<const f32x4*>(p);
-}
-template <bool DEV>
-__device__ __forceinline__ void st_part4(float* p, f32x4 x) {
-  if constexpr (DEV) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) st_dev(p + j, x[j]);
-  } else {
-    *reinterpret_cast<f32x4*>(p) = x;
-  }
-}
+// Cache policy of the partials of a merge inside a forward kernel: `sc1`
+// (device scope), coherent across the XCDs' L2 caches without the cache-wide
+// writeback and invalidate of a release/acquire fence.
+constexpr int kCpolSc1 = 16;
 
 // Row r, columns col..col+3 of the unit in part slot `unit` (of S splits),
 // written to the output element offset `off`.
-template <int DT, int D, bool DEV = false>
+template <int DT, int D>
 __device__ __forceinline__ void combine_row(const KArgs& a, int unit, int r, int col, int S,
                                             int64_t off) {
   const int64_t G = a.part_slots;
@@ -956,51 +931,38 @@ __device__ __forceinline__ void combine_row(const KArgs& a, int unit, int r, int
   const float* ml = a.part_ml + (static_cast<int64_t>(unit) * R + r) * 2;
   const float* po = a.part_o + (static_cast<int64_t>(unit) * R + r) * D + col;
   const int64_t ml_step = G * R * 2, o_step = G * R * D;  // one split further
-  auto ld = [&](const float* p) { return ld_part<DEV>(p); };
   float g = -INFINITY;
+  int s = 0;
+  for (; s + 4 <= S; s += 4) {
+    const float m0 = ml[(s + 0) * ml_step], m1 = ml[(s + 1) * ml_step];
+    const float m2 = ml[(s + 2) * ml_step], m3 = ml[(s + 3) * ml_step];
+    g = fmaxf(g, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
+  }
+  for (; s < S; ++s) g = fmaxf(g, ml[s * ml_step]);
+  const float g_use = (g == -INFINITY) ? 0.f : g;
   float lsum = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (DEV) {
-    // (the merge inside a forward kernel: one split at a time, the same
-    // operations in the same order as the loops below, in less code)
-    for (int s = 0; s < S; ++s) g = fmaxf(g, ld(ml + s * ml_step));
-    const float g_use = (g == -INFINITY) ? 0.f : g;
-    for (int s = 0; s < S; ++s) {
-      const float wgt = fast_exp2(ld(ml + s * ml_step) - g_use);
-      lsum += wgt * ld(ml + s * ml_step + 1);
-      acc += wgt * ld_part4<DEV>(po + s * o_step);
-    }
-  } else {
-    int s = 0;
-    for (; s + 4 <= S; s += 4) {
-      const float m0 = ld(ml + (s + 0) * ml_step), m1 = ld(ml + (s + 1) * ml_step);
-      const float m2 = ld(ml + (s + 2) * ml_step), m3 = ld(ml + (s + 3) * ml_step);
-      g = fmaxf(g, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-    }
-    for (; s < S; ++s) g = fmaxf(g, ld(ml + s * ml_step));
-    const float g_use = (g == -INFINITY) ? 0.f : g;
-    s = 0;
-    for (; s + 4 <= S; s += 4) {
-      float m[4], l[4];
-      f32x4 x[4];
+  s = 0;
+  for (; s + 4 <= S; s += 4) {
+    float m[4], l[4];
+    f32x4 x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        m[j] = ld(ml + (s + j) * ml_step);
-        l[j] = ld(ml + (s + j) * ml_step + 1);
-        x[j] = ld_part4<DEV>(po + (s + j) * o_step);
-      }
+    for (int j = 0; j < 4; ++j) {
+      m[j] = ml[(s + j) * ml_step];
+      l[j] = ml[(s + j) * ml_step + 1];
+      x[j] = *reinterpret_cast<const f32x4*>(po + (s + j) * o_step);
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {  // splits in order, as the one-at-a-time loop
-        const float wgt = fast_exp2(m[j] - g_use);
-        lsum += wgt * l[j];
-        acc += wgt * x[j];
-      }
+    for (int j = 0; j < 4; ++j) {  // splits in order, as the one-at-a-time loop
+      const float wgt = fast_exp2(m[j] - g_use);
+      lsum += wgt * l[j];
+      acc += wgt * x[j];
     }
-    for (; s < S; ++s) {
-      const float wgt = fast_exp2(ld(ml + s * ml_step) - g_use);
-      lsum += wgt * ld(ml + s * ml_step + 1);
-      acc += wgt * ld_part4<DEV>(po + s * o_step);
-    }
+  }
+  for (; s < S; ++s) {
+    const float wgt = fast_exp2(ml[s * ml_step] - g_use);
+    lsum += wgt * ml[s * ml_step + 1];
+    acc += wgt * *reinterpret_cast<const f32x4*>(po + s * o_step);
   }
   const float inv = 1.f / lsum;  // 0/0 -> NaN for a row with no key, as the reference
   if constexpr (DT == FA2_DTYPE_F32) {
@@ -1028,7 +990,7 @@ __global__ __launch_bounds__(kThreads) void fa2_combine_kernel(KArgs a) {
 }
 
 // Split merge inside the forward kernel (KArgs::merge_ctr).  The threads that
-// write this unit's partials do so with st_part4<true>; then every thread of
+// write this unit's partials do so with store_partial_rows<true>; then every thread of
 // the workgroup calls merge_publish (its stores have been performed at
 // device scope) and, after a workgroup barrier, merge_count; `flag` is one
 // LDS word of scratch.  merge_count returns true in every thread of the
@@ -1066,41 +1028,203 @@ __device__ __forceinline__ bool merge_count(const KArgs& a, int unit, int S, int
 
 // Split partials of one row (this lane's half: hi), the O^T accumulator
 // layout of the 16-bit kernels (row l32, dims 32d + 8g + 4hi + j at
-// o[d][4g + j]), into part slot `slot` (split * part_slots + unit).
+// o[d][4g + j]), into part slot `slot` (split * part_slots + unit); DEV:
+// written at device scope (`sc1` buffer stores) for a merge in the kernel.
 template <bool DEV, int D>
 __device__ __forceinline__ void store_partial_rows(const KArgs& a, int64_t slot, int r, int hi,
                                                    float m, float l, const f32x16 (&o)[D / 32]) {
-  if (hi == 0) {
-    float* ml = a.part_ml + (slot * a.part_rows + r) * 2;
-    if constexpr (DEV) {
-      st_dev(ml, m);
-      st_dev(ml + 1, l);
-    } else {
+  if constexpr (DEV) {
+    const uint32_t R = static_cast<uint32_t>(a.part_rows);
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc_uniform(a.part_ml + slot * R * 2, R * 8);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc_uniform(a.part_o + slot * R * D, R * D * 4);
+    if (hi == 0)
+      __builtin_amdgcn_raw_buffer_store_b64(
+          (u32x2){__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, l)}, rm,
+          static_cast<uint32_t>(r) * 8, 0, kCpolSc1);
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2],
+                                              o[d][g * 4 + 3]}),
+            ro, static_cast<uint32_t>(r * D + d * 32 + g * 8 + hi * 4) * 4, 0, kCpolSc1);
+  } else {
+    if (hi == 0) {
+      float* ml = a.part_ml + (slot * a.part_rows + r) * 2;
       ml[0] = m;
       ml[1] = l;
     }
+    float* po = a.part_o + (slot * a.part_rows + r) * D + hi * 4;
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(po + d * 32 + g * 8) =
+            (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]};
   }
-  float* po = a.part_o + (slot * a.part_rows + r) * D + hi * 4;
-#pragma unroll
-  for (int d = 0; d < D / 32; ++d)
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      st_part4<DEV>(po + d * 32 + g * 8,
-                    (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2], o[d][g * 4 + 3]});
 }
 
-// The merge itself: rows [0, rows) of the unit in part slot `unit`, the
-// output of row r at o_base + (row0 + r) * o_ss; NT threads of the workgroup.
-template <int DT, int D, int NT>
+// The merge itself: rows [0, rows) (rows <= MAXR) of the unit in part slot
+// `unit`, the output of row r at o_base + (row0 + r) * o_ss; NT threads of
+// the workgroup, each taking 4 columns of MAXR / (NT / (D / 4)) rows.  The
+// partials are read at device scope, a chunk of a thread's rows at once: with
+// at most SM splits, every split's (m, l) and O in one pass; otherwise the
+// running maxima of four splits at a time, then (m, l) and O split by split.
+// Per row and column the arithmetic is combine_row's, in the same order.
+// (The rows a thread holds at once are bounded for registers.)
+template <int DT, int D, int NT, int MAXR, int SM>
+__device__ __forceinline__ void merge_rows_sm(const KArgs& a, int unit, int S, int rows,
+                                              int64_t o_base, int row0) {
+  constexpr int kTPR = D / 4;
+  constexpr int kRPP = NT / kTPR;                   // rows per pass of the workgroup
+  constexpr int kRows = (MAXR + kRPP - 1) / kRPP;   // rows per thread
+  constexpr int kCap = (SM > 0 ? 16 / SM : 4) / (D > 128 ? 2 : 1);
+  constexpr int kIt = kRows < kCap ? kRows : kCap;  // rows per thread per chunk
+  const int col = (threadIdx.x % kTPR) * 4;
+  const int64_t G = a.part_slots;
+  const uint32_t R = static_cast<uint32_t>(a.part_rows);
+  auto rsrc_ml = [&](int s) {
+    return make_rsrc_uniform(a.part_ml + (s * G + unit) * static_cast<int64_t>(R) * 2, R * 8);
+  };
+  auto rsrc_o = [&](int s) {
+    return make_rsrc_uniform(a.part_o + (s * G + unit) * static_cast<int64_t>(R) * D, R * D * 4);
+  };
+  auto ld_ml = [&](__amdgpu_buffer_rsrc_t rs, int r) {
+    return __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<uint32_t>(r) * 8, 0, kCpolSc1);
+  };
+  auto ld_o = [&](__amdgpu_buffer_rsrc_t rs, int r) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<uint32_t>(r * D + col) * 4, 0,
+                                                 kCpolSc1);
+  };
+  // (bit_cast through scalars: this compiler reads element 0 when bit_cast
+  // is applied to a subscripted vector element)
+  auto fl = [](uint32_t w) { return __builtin_bit_cast(float, w); };
+  for (int c0 = threadIdx.x / kTPR; c0 < rows; c0 += kIt * kRPP) {  // chunks of kIt rows
+    float g[kIt], lsum[kIt];
+    f32x4 acc[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      g[it] = -INFINITY;
+      lsum[it] = 0.f;
+      acc[it] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    if constexpr (SM > 0) {
+      u32x2 ml[SM][kIt];
+      u32x4 x[SM][kIt];
+#pragma unroll
+      for (int s = 0; s < SM; ++s) {
+        if (s < S) {
+          const __amdgpu_buffer_rsrc_t rm = rsrc_ml(s);
+          const __amdgpu_buffer_rsrc_t ro = rsrc_o(s);
+#pragma unroll
+          for (int it = 0; it < kIt; ++it) {
+            if (c0 + it * kRPP < rows) {
+              ml[s][it] = ld_ml(rm, c0 + it * kRPP);
+              x[s][it] = ld_o(ro, c0 + it * kRPP);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        if (c0 + it * kRPP >= rows) continue;
+#pragma unroll
+        for (int s = 0; s < SM; ++s) {
+          const uint32_t mw = ml[s][it][0];
+          if (s < S) g[it] = fmaxf(g[it], fl(mw));
+        }
+        const float g_use = g[it] == -INFINITY ? 0.f : g[it];
+#pragma unroll
+        for (int s = 0; s < SM; ++s) {
+          if (s < S) {
+            const uint32_t mw = ml[s][it][0], lw = ml[s][it][1];
+            const float wgt = fast_exp2(fl(mw) - g_use);
+            lsum[it] += wgt * fl(lw);
+            acc[it] += wgt * __builtin_bit_cast(f32x4, x[s][it]);
+          }
+        }
+      }
+    } else {
+      int s = 0;
+      for (; s + 4 <= S; s += 4) {
+        float m[4][kIt];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const __amdgpu_buffer_rsrc_t rs = rsrc_ml(s + j);
+#pragma unroll
+          for (int it = 0; it < kIt; ++it) {
+            const uint32_t mw = c0 + it * kRPP < rows ? ld_ml(rs, c0 + it * kRPP)[0] : 0u;
+            m[j][it] = c0 + it * kRPP < rows ? fl(mw) : -INFINITY;
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it)
+          g[it] = fmaxf(g[it], fmaxf(fmaxf(m[0][it], m[1][it]), fmaxf(m[2][it], m[3][it])));
+      }
+      for (; s < S; ++s) {
+        const __amdgpu_buffer_rsrc_t rs = rsrc_ml(s);
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          if (c0 + it * kRPP < rows) {
+            const uint32_t mw = ld_ml(rs, c0 + it * kRPP)[0];
+            g[it] = fmaxf(g[it], fl(mw));
+          }
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < kIt; ++it)
+        if (g[it] == -INFINITY) g[it] = 0.f;  // (g_use)
+      for (s = 0; s < S; ++s) {
+        const __amdgpu_buffer_rsrc_t rm = rsrc_ml(s);
+        const __amdgpu_buffer_rsrc_t ro = rsrc_o(s);
+        u32x2 ml[kIt];
+        u32x4 x[kIt];
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          if (c0 + it * kRPP < rows) {
+            ml[it] = ld_ml(rm, c0 + it * kRPP);
+            x[it] = ld_o(ro, c0 + it * kRPP);
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          if (c0 + it * kRPP < rows) {
+            const uint32_t mw = ml[it][0], lw = ml[it][1];
+            const float wgt = fast_exp2(fl(mw) - g[it]);
+            lsum[it] += wgt * fl(lw);
+            acc[it] += wgt * __builtin_bit_cast(f32x4, x[it]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int r = c0 + it * kRPP;
+      if (r >= rows || col >= a.dv) continue;
+      const float inv = 1.f / lsum[it];  // 0/0 -> NaN for a row with no key, as the reference
+      const int64_t off = o_base + static_cast<int64_t>(row0 + r) * a.o_ss + col;
+      if constexpr (DT == FA2_DTYPE_F32) {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + off) = acc[it] * inv;
+      } else {
+        constexpr bool BF = Elt<DT>::kBF;
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + off) =
+            (u32x2){pack2<BF>(acc[it][0] * inv, acc[it][1] * inv),
+                    pack2<BF>(acc[it][2] * inv, acc[it][3] * inv)};
+      }
+    }
+  }
+}
+
+template <int DT, int D, int NT, int MAXR>
 __device__ __forceinline__ void merge_rows(const KArgs& a, int unit, int S, int rows,
                                            int64_t o_base, int row0) {
-  constexpr int kTPR = D / 4;
-  constexpr int kRowsPerPass = NT / kTPR;
-  const int col = (threadIdx.x % kTPR) * 4;
-  if (col >= a.dv) return;
-  for (int r = threadIdx.x / kTPR; r < rows; r += kRowsPerPass)
-    combine_row<DT, D, true>(a, unit, r, col, S,
-                             o_base + static_cast<int64_t>(row0 + r) * a.o_ss + col);
+  if (S <= 2)
+    merge_rows_sm<DT, D, NT, MAXR, 2>(a, unit, S, rows, o_base, row0);
+  else if (S <= 4)
+    merge_rows_sm<DT, D, NT, MAXR, 4>(a, unit, S, rows, o_base, row0);
+  else
+    merge_rows_sm<DT, D, NT, MAXR, 0>(a, unit, S, rows, o_base, row0);
 }
 
 // ---------------------------------------------------------------------------

@@ -410,31 +410,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
     const int64_t slot_id = static_cast<int64_t>(split) * a.part_slots + blockIdx.x;
     const int r = rc * kWaveRows + l32;
     // (read by the merge of this kernel at device scope, or by the combine)
-    auto store = [&](auto dev) {
-      constexpr bool DEV = decltype(dev)::value;
-      if (hi == 0) {
-        float* ml = a.part_ml + (slot_id * a.part_rows + r) * 2;
-        if constexpr (DEV) {
-          st_dev(ml, m_all);
-          st_dev(ml + 1, l_sum);
-        } else {
-          ml[0] = m_all;
-          ml[1] = l_sum;
-        }
-      }
-      float* pout = a.part_o + (slot_id * a.part_rows + r) * D + hi * 4;
-#pragma unroll
-      for (int d = 0; d < DB; ++d)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          st_part4<DEV>(pout + d * 32 + g * 8, (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1],
-                                                       o[d][g * 4 + 2], o[d][g * 4 + 3]});
-    };
     if (qrow < w.Lq && r < a.part_rows) {
       if (a.merge_ctr)
-        store(std::true_type{});
+        store_partial_rows<true, D>(a, slot_id, r, hi, m_all, l_sum, o);
       else
-        store(std::false_type{});
+        store_partial_rows<false, D>(a, slot_id, r, hi, m_all, l_sum, o);
     }
   }
   if (!a.merge_ctr) return;  // the combine kernel merges
@@ -442,7 +422,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa2_decode_kernel(KArgs a) {
   merge_publish();
   __syncthreads();
   if (!merge_count(a, blockIdx.x, S, counters + 2 * NS + 1)) return;
-  merge_rows<DT, D, kDecThreads>(a, blockIdx.x, S, min(a.part_rows, w.Lq - q0), w.o_base, q0);
+  merge_rows<DT, D, kDecThreads, kDecRows>(a, blockIdx.x, S, min(a.part_rows, w.Lq - q0),
+                                           w.o_base, q0);
 }
 
 }  // namespace fa2

@@ -795,7 +795,7 @@ __global__ __launch_bounds__(kThreads, D > 128 ? 1 : FA2_LDS_OCCUPANCY) void fa2
       merge_publish();
       __syncthreads();
       if (merge_count(a, blockIdx.x, S, &merge_flag))
-        merge_rows<DT, D, kThreads>(a, blockIdx.x, S, min(a.part_rows, w.Lq - q0), w.o_base,
+        merge_rows<DT, D, kThreads, kBM>(a, blockIdx.x, S, min(a.part_rows, w.Lq - q0), w.o_base,
                                     q0);
     }
   }

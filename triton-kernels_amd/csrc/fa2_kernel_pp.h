@@ -618,9 +618,10 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       if (merge_count(a, unit0, S, &merge_flag)) {
         const int q0 = w.qblk * kBM;
         const int rows = min(kBM, w.Lq - q0);
-        merge_rows<DT, D, kPPThreads>(a, unit0, S, rows, w.o_base, q0);
+        merge_rows<DT, D, kPPThreads, kBM>(a, unit0, S, rows, w.o_base, q0);
         if (w.hg + 1 < group)
-          merge_rows<DT, D, kPPThreads>(a, unit0 + kXcds, S, rows, w.o_base + a.o_sh, q0);
+          merge_rows<DT, D, kPPThreads, kBM>(a, unit0 + kXcds, S, rows, w.o_base + a.o_sh,
+                                                q0);
       }
     }
 
