@@ -332,6 +332,8 @@ def main(argv=None):
     ap.add_argument("--sweep-only", default=None, metavar="TERMS",
                     help="comma-separated terms (e.g. 'ragged,bf16,q128,kv128'): run only the "
                          "sweep points whose description holds every term")
+    ap.add_argument("--kernel", default="auto", choices=["auto", "regular", "short"],
+                    help="prefill configs: flash_attention_v2's kernel choice (fa2_params.kernel)")
     ap.add_argument("--host-cost", type=int, default=0, metavar="N",
                     help="only time the host side of N back-to-back calls of the config's "
                          "step (launch extension and ctypes paths), with their GPU time")
@@ -410,6 +412,11 @@ def main(argv=None):
         w_cpu = W.spread_pool(w_cpu, args.pool_gib)
     w = w_cpu.to(dev)
     kw = w.kwargs()
+    if args.kernel != "auto":
+        if w.kind != "prefill":
+            print("bench.py: --kernel applies to prefill configs only", file=sys.stderr)
+            return 2
+        kw["kernel"] = args.kernel
     fl = W.flops(w)
     nbytes = W.hbm_bytes(w)
     flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if args.flush else None
@@ -501,6 +508,7 @@ def main(argv=None):
             "algorithmic_mb_per_step": round(nbytes / 1e6, 2),
             "l2_mall_flushed": bool(args.flush),
             **({"large_pool": pool_check} if pool_check else {}),
+            **({"kernel": args.kernel} if args.kernel != "auto" else {}),
             "parallelism": "single GPU",
         },
         "roofline": {
