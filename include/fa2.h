@@ -143,7 +143,12 @@ typedef struct fa2_params {
    * counterpart in the reference (its grid is fixed by :873-880). */
   int32_t max_workgroups;
 
-  void* workspace;              /* device scratch, >= fa2_fwd_workspace_size */
+  /* Device scratch, >= fa2_fwd_workspace_size (fa2_decode_workspace_size),
+   * with any prior content: it never needs clearing.  (A call that merges its
+   * splits inside the forward kernel counts them in words tagged per call and
+   * leaves them at zero for a replay of itself.)  One workspace per call in
+   * flight. */
+  void* workspace;
   size_t workspace_bytes;
 
   /* An upper bound of every sequence's KV length, or 0 if unknown (paged:
