@@ -921,6 +921,18 @@ constexpr int kCombineRows = kThreads / (D / 4);  // rows per workgroup
 // writeback and invalidate of a release/acquire fence.
 constexpr int kCpolSc1 = 16;
 
+// Device-scope stores of partials from per-lane addresses (relaxed
+// agent-scope atomic stores: `global_store_dword ... sc1`).
+__device__ __forceinline__ void st_dev2(float* p, float x, float y) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(p + 1, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev4(float* p, f32x4 x) {
+  const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  st_dev2(p, x0, x1);
+  st_dev2(p + 2, x2, x3);
+}
+
 // Row r, columns col..col+3 of the unit in part slot `unit` (of S splits),
 // written to the output element offset `off`.
 template <int DT, int D>

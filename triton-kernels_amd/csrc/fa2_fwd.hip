@@ -21,6 +21,7 @@
 #include "fa2_kernel_pp.h"
 #include "fa2_kernel_short.h"
 #include "fa2_kernel_decode.h"
+#include "fa2_kernel_decode_f32.h"
 #include "fa2_kernel_f32.h"
 #include "fa2_kv_append.h"
 
@@ -52,6 +53,11 @@
 #ifndef FA2_DECODE_FOLD
 #define FA2_DECODE_FOLD 1
 #endif
+// 1: fp32 decode units of at most kDecF32MaxRows rows run the VALU decode
+// kernel (see make_plan_packed); 0: the fp32-MFMA kernel
+#ifndef FA2_DECODE_F32_VALU
+#define FA2_DECODE_F32_VALU 1
+#endif
 // 1: ragged launches that fit the GPU at once run without the plan kernel
 // and merge their own splits (see make_plan); 0: plan and combine launches
 #ifndef FA2_INLINE_PLAN
@@ -65,6 +71,13 @@ namespace {
 // aim at this many workgroups per CU, keeping this many KV tiles per split
 constexpr int64_t kF32DecodeWgsPerCu = 8;
 constexpr int64_t kF32DecodeMinTiles = 32;
+// the VALU fp32 decode kernel (two workgroups per CU): workgroups per CU and
+// KV tiles per split its automatic splits aim at.  Measured on MI355X (us per
+// call at 1 / 2 / 4 / 8 / 16 forced splits): d1 263 / 153 / 130 / 135 / 151,
+// s1 464 / 250 / 163 / 171 / 195, d2 634 / 480 / 492 / 526 / 607; these
+// constants pick 4, 4 and 2.
+constexpr int64_t kDecF32WgsPerCu = 4;
+constexpr int64_t kDecF32MinTiles = 32;
 
 // byte offset of the kXcds claim counters after the work list's item count
 // (within the 256 bytes reserved there; a cache line of their own)
@@ -119,6 +132,7 @@ struct Plan {
   int block_rows;   // rows per q-block of the launched kernel
   bool dec;         // packed fp16/bf16: the decode kernel
   bool f32;         // fp32 arithmetic: the fp32-MFMA kernel
+  bool decf32;      // packed fp32 with few rows per unit: the VALU decode kernel
   bool conv;        // fp32 tensors with the reference's fp16 rounding: fp16 copies in the
                     // workspace, the 16-bit kernels, partials and an fp32 combine
   bool plan;        // ragged/paged: the plan kernel orders the work list
@@ -334,6 +348,7 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv 
   pl->block_rows = kBM;
   pl->dec = false;
   pl->f32 = p->dtype == FA2_DTYPE_F32 && p->arith == FA2_ARITH_FP32;
+  pl->decf32 = false;
   pl->plan = p->layout != FA2_LAYOUT_DENSE;
   // The split count above rests on the longest KV sweep any sequence can
   // have; for ragged K/V that is the total of all sequences (the lengths
@@ -435,7 +450,11 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   pl->dec = p->dtype != FA2_DTYPE_F32 && fast_dim(p->head_dim);
   pl->f32 = p->dtype == FA2_DTYPE_F32;  // decode's reference computes fp32 in fp32
   pl->conv = false;
-  pl->block_rows = pl->dec ? kDecRows : kBM;
+  // fp32 units of at most kDecF32MaxRows rows: the VALU decode kernel, whose
+  // units hold 4 or 8 rows
+  pl->decf32 = FA2_DECODE_F32_VALU && pl->f32 &&
+               (p->head_dim == 64 || p->head_dim == 128) && pl->rows <= kDecF32MaxRows;
+  pl->block_rows = pl->dec ? kDecRows : (pl->decf32 ? (pl->rows <= 4 ? 4 : 8) : kBM);
   const int64_t nqb = cdiv(pl->rows, pl->block_rows);
   pl->work_ub = nqb * p->batch;
   pl->npairs = pl->work_ub * p->kv_heads;
@@ -457,8 +476,9 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
     // 4 / 8 workgroups per CU and >= 8 tiles: d1 (128 units of 128 tiles)
     // 338 / 180 / 187 / 204 at 2 / 4 / 8 / 16 splits; d2 (512 units, up to
     // 128 tiles) 1730 / 1731 / 1148 / 1105 at 1 / 1 / 2 / 4 splits).
-    const int64_t target = pl->dec ? cus : cus * kF32DecodeWgsPerCu;
-    const int64_t min_tiles = pl->dec ? 8 : kF32DecodeMinTiles;
+    const int64_t target =
+        pl->dec ? cus : (pl->decf32 ? cus * kDecF32WgsPerCu : cus * kF32DecodeWgsPerCu);
+    const int64_t min_tiles = pl->dec ? 8 : (pl->decf32 ? kDecF32MinTiles : kF32DecodeMinTiles);
     const int64_t tiles = cdiv(kv_upper_bound(p), kBN);
     splits = 1;
     if (pl->npairs > 0 && pl->npairs < target) {
@@ -485,7 +505,7 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
     pl->plan = false;
   // The decode kernel merges its own splits: the last split of a unit to
   // finish combines the unit's partials, so no combine launch follows.
-  pl->fold = FA2_DECODE_FOLD && pl->dec && splits > 1;
+  pl->fold = FA2_DECODE_FOLD && (pl->dec || pl->decf32) && splits > 1;
   pl->inline_plan = false;
   return finish_plan(p, pl);
 }
@@ -539,6 +559,21 @@ int launch_typed(KArgs a, const Plan& pl, hipStream_t st) {
                          const_cast<int2*>(a.work), const_cast<int32_t*>(a.work_count));
   }
   const dim3 grid(pl.grid_x, pl.splits);
+  if constexpr (DT == FA2_DTYPE_F32 && (D == 64 || D == 128)) {
+    if (pl.decf32) {
+      if (pl.block_rows == 4)
+        hipLaunchKernelGGL((fa2_decode_f32_kernel<D, MODE, 4>), grid, dim3(kDecF32Threads), 0, st,
+                           a);
+      else
+        hipLaunchKernelGGL((fa2_decode_f32_kernel<D, MODE, 8>), grid, dim3(kDecF32Threads), 0, st,
+                           a);
+      if (pl.splits > 1 && !pl.fold)
+        hipLaunchKernelGGL((fa2_combine_kernel<DT, D, MODE>),
+                           dim3(pl.grid_x, cdiv(pl.part_rows, kCombineRows<D>)), dim3(kThreads),
+                           0, st, a);
+      return hipGetLastError() == hipSuccess ? FA2_OK : FA2_ERR_HIP;
+    }
+  }
   if constexpr (DT == FA2_DTYPE_F32) {
     if (pl.f32) {
       FA2_LAUNCH_BUF(fa2_fwd_f32_kernel, grid, dim3(kThreads));
