@@ -326,6 +326,9 @@ struct Work {
 // sequence by sequence; every workgroup of such a launch is resident at once,
 // so the order of the items does not matter.
 constexpr int kInlinePlanMaxBatch = 256;
+// Balanced walk of the two-head kernel: kv-head pairs per lane of the wave
+// that locates a workgroup's segment (at most 64 * kBalMaxPer per XCD).
+constexpr int kBalMaxPer = 16;
 struct InlinePlan {
   int cum[kInlinePlanMaxBatch + 1];
   int qi[kInlinePlanMaxBatch + 1];  // copies of q_indptr and kv_indptr
@@ -1077,16 +1080,89 @@ __device__ __forceinline__ void store_partial_rows(const KArgs& a, int64_t slot,
   }
 }
 
-// The merge itself: rows [0, rows) (rows <= MAXR) of the unit in part slot
-// `unit`, the output of row r at o_base + (row0 + r) * o_ss; NT threads of
-// the workgroup, each taking 4 columns of MAXR / (NT / (D / 4)) rows.  The
-// partials are read at device scope, a chunk of a thread's rows at once: with
-// at most SM splits, every split's (m, l) and O in one pass; otherwise the
-// running maxima of four splits at a time, then (m, l) and O split by split.
-// Per row and column the arithmetic is combine_row's, in the same order.
+// Partials in fragment order (the two-head kernel's balanced walk): wave wq's
+// (m, l) of row wq * 32 + l32 at that row, and its O^T accumulator o[d]
+// (dims 32d + 8g + 4hi + j at o[d][4g + j]) at chunk ((wq * D / 32 + d) * 4 +
+// g) * 64 + lane of 16 bytes, so that one store or load of the wave covers
+// 1 KB in a row.  Written and read at device scope (sc1) by the workgroups
+// of one unit's pieces; only they read this layout.
+template <int D>
+__device__ __forceinline__ void store_partial_frag(const KArgs& a, int64_t slot, int wq,
+                                                   int lane, float m, float l,
+                                                   const f32x16 (&o)[D / 32]) {
+  const uint32_t R = static_cast<uint32_t>(a.part_rows);
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc_uniform(a.part_ml + slot * R * 2, R * 8);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc_uniform(a.part_o + slot * R * D, R * D * 4);
+  if (lane < 32)
+    __builtin_amdgcn_raw_buffer_store_b64(
+        (u32x2){__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, l)}, rm,
+        static_cast<uint32_t>(wq * 32 + lane) * 8, 0, kCpolSc1);
+#pragma unroll
+  for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(u32x4, (f32x4){o[d][g * 4 + 0], o[d][g * 4 + 1], o[d][g * 4 + 2],
+                                            o[d][g * 4 + 3]}),
+          ro, static_cast<uint32_t>(((wq * (D / 32) + d) * 4 + g) * 64 + lane) * 16, 0,
+          kCpolSc1);
+}
+
+// (m, l) of this lane's row from a fragment-order slot
+__device__ __forceinline__ u32x2 load_partial_frag_ml(const KArgs& a, int64_t slot, int wq,
+                                                      int l32) {
+  const uint32_t R = static_cast<uint32_t>(a.part_rows);
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc_uniform(a.part_ml + slot * R * 2, R * 8);
+  return __builtin_amdgcn_raw_buffer_load_b64(rm, static_cast<uint32_t>(wq * 32 + l32) * 8, 0,
+                                              kCpolSc1);
+}
+
+// O^T block d of this lane from a fragment-order slot
+template <int D>
+__device__ __forceinline__ f32x16 load_partial_frag_o(const KArgs& a, int64_t slot, int wq,
+                                                      int lane, int d) {
+  const uint32_t R = static_cast<uint32_t>(a.part_rows);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc_uniform(a.part_o + slot * R * D, R * D * 4);
+  f32x16 x;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4 c = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                   ro, static_cast<uint32_t>(((wq * (D / 32) + d) * 4 + g) * 64 + lane) * 16, 0,
+                   kCpolSc1));
+    x[g * 4 + 0] = c[0];
+    x[g * 4 + 1] = c[1];
+    x[g * 4 + 2] = c[2];
+    x[g * 4 + 3] = c[3];
+  }
+  return x;
+}
+
+// A unit's merge word (merge_count's) when every other piece has counted:
+// the caller is the last piece and takes the word back to (tag, 0) without
+// having written its partials.  Thread 0; true if taken.
+__device__ __forceinline__ bool merge_take_last(const KArgs& a, int unit, int S) {
+  uint64_t* c = a.merge_ctr + unit;
+  const uint64_t tag = a.merge_tag;
+  uint64_t old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t cnt =
+      (old >> kMergeCountBits) == tag ? (old & ((uint64_t(1) << kMergeCountBits) - 1)) : 0;
+  if (static_cast<int>(cnt) + 1 != S) return false;
+  return __hip_atomic_compare_exchange_strong(c, &old, tag << kMergeCountBits, __ATOMIC_RELAXED,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The merge itself: rows [0, rows) (rows <= MAXR) of the partials of
+// pieces 0..S-1, piece s in part slot slot_of(s), the output of row r at
+// o_base + (row0 + r) * o_ss; NT threads of the workgroup, each taking 4
+// columns of MAXR / (NT / (D / 4)) rows.  The partials are read at device
+// scope, a chunk of a thread's rows at once: with at most SM pieces, every
+// piece's (m, l) and O in one pass; otherwise the running maxima of four
+// pieces at a time, then (m, l) and O piece by piece.  Per row and column
+// the arithmetic is combine_row's, in the same order.
 // (The rows a thread holds at once are bounded for registers.)
-template <int DT, int D, int NT, int MAXR, int SM>
-__device__ __forceinline__ void merge_rows_sm(const KArgs& a, int unit, int S, int rows,
+template <int DT, int D, int NT, int MAXR, int SM, typename SlotOf>
+__device__ __forceinline__ void merge_rows_sm(const KArgs& a, SlotOf slot_of, int S, int rows,
                                               int64_t o_base, int row0) {
   constexpr int kTPR = D / 4;
   constexpr int kRPP = NT / kTPR;                   // rows per pass of the workgroup
@@ -1094,13 +1170,12 @@ __device__ __forceinline__ void merge_rows_sm(const KArgs& a, int unit, int S, i
   constexpr int kCap = (SM > 0 ? 16 / SM : 4) / (D > 128 ? 2 : 1);
   constexpr int kIt = kRows < kCap ? kRows : kCap;  // rows per thread per chunk
   const int col = (threadIdx.x % kTPR) * 4;
-  const int64_t G = a.part_slots;
   const uint32_t R = static_cast<uint32_t>(a.part_rows);
   auto rsrc_ml = [&](int s) {
-    return make_rsrc_uniform(a.part_ml + (s * G + unit) * static_cast<int64_t>(R) * 2, R * 8);
+    return make_rsrc_uniform(a.part_ml + slot_of(s) * static_cast<int64_t>(R) * 2, R * 8);
   };
   auto rsrc_o = [&](int s) {
-    return make_rsrc_uniform(a.part_o + (s * G + unit) * static_cast<int64_t>(R) * D, R * D * 4);
+    return make_rsrc_uniform(a.part_o + slot_of(s) * static_cast<int64_t>(R) * D, R * D * 4);
   };
   auto ld_ml = [&](__amdgpu_buffer_rsrc_t rs, int r) {
     return __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<uint32_t>(r) * 8, 0, kCpolSc1);
@@ -1228,15 +1303,25 @@ __device__ __forceinline__ void merge_rows_sm(const KArgs& a, int unit, int S, i
   }
 }
 
+// pieces in arbitrary part slots (slot_of(s), s < S)
+template <int DT, int D, int NT, int MAXR, typename SlotOf>
+__device__ __forceinline__ void merge_rows_at(const KArgs& a, SlotOf slot_of, int S, int rows,
+                                              int64_t o_base, int row0) {
+  if (S <= 2)
+    merge_rows_sm<DT, D, NT, MAXR, 2>(a, slot_of, S, rows, o_base, row0);
+  else if (S <= 4)
+    merge_rows_sm<DT, D, NT, MAXR, 4>(a, slot_of, S, rows, o_base, row0);
+  else
+    merge_rows_sm<DT, D, NT, MAXR, 0>(a, slot_of, S, rows, o_base, row0);
+}
+
+// the splits of one unit: split s in slot s * part_slots + unit
 template <int DT, int D, int NT, int MAXR>
 __device__ __forceinline__ void merge_rows(const KArgs& a, int unit, int S, int rows,
                                            int64_t o_base, int row0) {
-  if (S <= 2)
-    merge_rows_sm<DT, D, NT, MAXR, 2>(a, unit, S, rows, o_base, row0);
-  else if (S <= 4)
-    merge_rows_sm<DT, D, NT, MAXR, 4>(a, unit, S, rows, o_base, row0);
-  else
-    merge_rows_sm<DT, D, NT, MAXR, 0>(a, unit, S, rows, o_base, row0);
+  const int64_t G = a.part_slots;
+  merge_rows_at<DT, D, NT, MAXR>(
+      a, [=](int s) { return static_cast<int64_t>(s) * G + unit; }, S, rows, o_base, row0);
 }
 
 // ---------------------------------------------------------------------------

@@ -45,6 +45,11 @@
 #endif
 // 1: ragged/paged two-head launches claim units from per-XCD counters
 // (KArgs::claim); 0: the static round walk
+// 1: paged calls with one q-block per sequence and more two-head units than
+// CUs take the balanced walk (see make_plan); 0: rounds of whole units
+#ifndef FA2_PP_BAL
+#define FA2_PP_BAL 1
+#endif
 #ifndef FA2_PP_CLAIM
 #define FA2_PP_CLAIM 1
 #endif
@@ -140,6 +145,8 @@ struct Plan {
   bool buf;         // paged: every row of the pool has a 31-bit byte offset
   bool fold;        // splits merged by the forward kernel (KArgs::merge_ctr), no combine
   bool inline_plan; // ragged without the plan kernel (KArgs::inline_plan)
+  bool bal;         // paged: the two-head kernel's balanced walk (pp_bal_locate)
+  int64_t bal_slots;  // ... its part slots (4 per workgroup)
   int64_t max_wgs;  // cap on the persistent grid (0: none)
   uint32_t pool_bytes_k, pool_bytes_v;
   size_t off_work, off_count, off_ml, off_o, off_ctr, off_cq, off_ck, off_cv, total;
@@ -246,7 +253,8 @@ int64_t kv_upper_bound(const fa2_params* p) {
   return ub;
 }
 
-int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv = true) {
+int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv = true,
+              bool allow_bal = true) {
   const int64_t nqb = cdiv(p->q_len, kBM);
   // fp32 tensors of flash_attention_v2, whose reference rounds every operand
   // to fp16 (attention.py:547, 569, 621) and keeps fp32 partials that a
@@ -392,6 +400,29 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv 
       pl->fold = splits > 1;
     }
   }
+  // Paged calls with one q-block per sequence and more two-head units than
+  // CUs: the balanced walk instead of rounds of whole units, so that no
+  // workgroup runs more than its share of the KV tiles (fa2_kernel_pp.h).
+  // Whole units leave the longest workgroup at the sum of its two units,
+  // which unequal lengths push well past the mean: c4 (32 sequences of
+  // 512-8192 keys, 128 new rows each, Hq32/Hkv8 D128), 164 tiles against a
+  // mean of 138.  No plan kernel: the units are in (sequence, kv head)
+  // order.  Each workgroup's stream is one head pair of one XCD, so the
+  // workgroups per XCD are a multiple of the head pairs.
+  pl->bal = false;
+  pl->bal_slots = 0;
+  if (FA2_PP_BAL && allow_bal && p->layout == FA2_LAYOUT_PAGED && pl->pp && !pl->qpair &&
+      !pl->shortk && splits == 1 && p->num_splits == 0 && p->max_workgroups == 0 && nqb == 1) {
+    const int64_t cus = query_device ? cu_count_current_device() : 256;
+    const int64_t upp = cdiv(group, 2);
+    const int64_t tiles = cdiv(kv_upper_bound(p), kBN) + 1;
+    if (pl->grid_pp > cus && cus % kXcds == 0 && (cus / kXcds) % upp == 0 &&
+        pl->npairs <= kXcds * 64 * kBalMaxPer && tiles * cdiv(pl->npairs, kXcds) < (1 << 30)) {
+      pl->bal = true;
+      pl->plan = false;
+      pl->bal_slots = 4 * cus;
+    }
+  }
   return finish_plan(p, pl);
 }
 
@@ -401,6 +432,11 @@ int finish_plan(const fa2_params* p, Plan* pl) {
   pl->pool_bytes_k = pl->pool_bytes_v = 0;
   pl->buf = buffer_path_ok(p, &pl->pool_bytes_k, &pl->pool_bytes_v);
   pl->max_wgs = p->max_workgroups;
+  if (pl->bal && !pl->buf) {  // (built for the buffer path only)
+    pl->bal = false;
+    pl->bal_slots = 0;
+    pl->plan = true;
+  }
 
   size_t off = 0;
   pl->off_work = off;
@@ -410,16 +446,16 @@ int finish_plan(const fa2_params* p, Plan* pl) {
   if (p->layout != FA2_LAYOUT_DENSE) off += 256;
   const bool parts = splits > 1 || pl->conv;
   if (!parts) pl->fold = false;
-  pl->off_ctr = off;  // one merge word per part slot
-  if (pl->fold) off += static_cast<size_t>(pl->grid_x) * sizeof(uint64_t);
+  pl->off_ctr = off;  // one merge word per one-head unit
+  if (pl->fold || pl->bal) off += static_cast<size_t>(pl->grid_x) * sizeof(uint64_t);
   off = (off + 255) & ~size_t(255);
+  const size_t slots =
+      pl->bal ? static_cast<size_t>(pl->bal_slots) : parts ? static_cast<size_t>(splits) * pl->grid_x : 0;
   pl->off_ml = off;
-  if (parts)
-    off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * 2 * sizeof(float);
+  off += slots * pl->part_rows * 2 * sizeof(float);
   off = (off + 255) & ~size_t(255);
   pl->off_o = off;
-  if (parts)
-    off += static_cast<size_t>(splits) * pl->grid_x * pl->part_rows * pl->dim * sizeof(float);
+  off += slots * pl->part_rows * pl->dim * sizeof(float);
   // fp16 copies: q [B][Hq][Lq][D] or [Tq][Hq][D], k and v likewise
   const int64_t qrows = p->layout == FA2_LAYOUT_DENSE ? p->batch * p->q_len : p->q_len;
   const int64_t kvrows = p->layout == FA2_LAYOUT_DENSE ? p->batch * p->kv_len : p->kv_len;
@@ -507,6 +543,8 @@ int make_plan_packed(const fa2_params* p, Plan* pl, bool query_device) {
   // finish combines the unit's partials, so no combine launch follows.
   pl->fold = FA2_DECODE_FOLD && (pl->dec || pl->decf32) && splits > 1;
   pl->inline_plan = false;
+  pl->bal = false;
+  pl->bal_slots = 0;
   return finish_plan(p, pl);
 }
 
@@ -614,6 +652,10 @@ int launch_typed(KArgs a, const Plan& pl, hipStream_t st) {
             else if (MODE == FA2_LAYOUT_RAGGED && a.inline_plan)
               hipLaunchKernelGGL((fa2_fwd_pp_kernel<DT, D, FA2_LAYOUT_RAGGED, true, false, true>),
                                  gpp, dim3(kPPThreads), 0, st, a);
+            else if (MODE == FA2_LAYOUT_PAGED && pl.bal)
+              hipLaunchKernelGGL(
+                  (fa2_fwd_pp_kernel<DT, D, FA2_LAYOUT_PAGED, true, false, false, true>), gpp,
+                  dim3(kPPThreads), 0, st, a);
             else
               FA2_LAUNCH_BUF(fa2_fwd_pp_kernel, gpp, dim3(kPPThreads));
           } else {
@@ -699,7 +741,7 @@ int workspace_size(const fa2_params* p, size_t* bytes, bool packed) {
     *bytes = 0;
     return FA2_OK;
   }
-  Plan pl;
+  Plan pl{};
   s = packed ? make_plan_packed(p, &pl, p->num_splits == 0)
              : make_plan(p, &pl, p->num_splits == 0);
   if (s != FA2_OK) return s;
@@ -730,7 +772,7 @@ int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) 
   if (!p->q || !p->k || !p->v || !p->o) return FA2_ERR_NULL_POINTER;
   if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o))
     return FA2_ERR_ALIGNMENT;
-  Plan pl;
+  Plan pl{};
   s = packed ? make_plan_packed(p, &pl, p->num_splits == 0)
              : make_plan(p, &pl, p->num_splits == 0, allow_conv);
   if (s != FA2_OK) return s;
@@ -777,12 +819,13 @@ int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) 
   a.work = pl.plan ? reinterpret_cast<const int2*>(ws + pl.off_work) : nullptr;
   a.work_count = pl.plan ? reinterpret_cast<const int32_t*>(ws + pl.off_count) : nullptr;
   a.split_count = pl.dev_splits ? reinterpret_cast<int32_t*>(ws + pl.off_count) + 1 : nullptr;
-  const bool parts = pl.splits > 1 || pl.conv;
+  const bool parts = pl.splits > 1 || pl.conv || pl.bal;
   a.part_ml = parts ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
   a.part_o = parts ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
   a.part_rows = pl.part_rows;
-  a.merge_ctr = pl.fold ? reinterpret_cast<uint64_t*>(ws + pl.off_ctr) : nullptr;
-  a.merge_tag = pl.fold ? next_merge_tag() : 0;
+  const bool merges = pl.fold || pl.bal;
+  a.merge_ctr = merges ? reinterpret_cast<uint64_t*>(ws + pl.off_ctr) : nullptr;
+  a.merge_tag = merges ? next_merge_tag() : 0;
   a.inline_plan = pl.inline_plan ? 1 : 0;
   a.auto_splits = p->num_splits == 0 ? 1 : 0;
   a.pack_m = packed ? static_cast<int32_t>(p->q_len) : 0;
@@ -905,7 +948,7 @@ extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
   if (empty_problem(p)) return FA2_OK;
   constexpr size_t cap = FA2_NOALLOC_SCRATCH_BYTES;
   fa2_params c = *p;
-  Plan pl;
+  Plan pl{};
   // The plan with fp16 copies of fp32 tensors (the faster kernel, and the
   // one fa2_fwd runs) comes first, with fewer automatic splits until its
   // workspace fits; fp32 tensors fall back to the register-staged kernel
@@ -914,6 +957,10 @@ extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
     c = *p;
     int r = make_plan(&c, &pl, c.num_splits == 0, allow_conv);
     if (r != FA2_OK) return r;
+    if (pl.bal && pl.total > cap) {  // whole units need no part slots
+      r = make_plan(&c, &pl, c.num_splits == 0, allow_conv, false);
+      if (r != FA2_OK) return r;
+    }
     if (p->num_splits == 0)
       for (int sp = pl.splits - 1; sp >= 1 && pl.total > cap; --sp) {
         c.num_splits = sp;

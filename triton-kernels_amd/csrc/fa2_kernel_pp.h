@@ -114,17 +114,90 @@ struct PPUnit {
   int T, t_begin, q0;
   int64_t q_base, o_base;  // this group's head
   bool hok;                // this group's head exists (odd head groups)
+  // balanced walk: the unit's start in its stream and its weight (KV tiles,
+  // at least 1), and whether this workgroup runs only a piece of it
+  int us, W;
+  bool part;
 };
+
+// Balanced walk (paged, one q-block per sequence, more units than
+// workgroups).  The units of XCD x (L = x mod kXcds) form Hq/Hkv/2 streams,
+// one per head pair g, over the kv-head pairs of the XCD in order, unit
+// (j, g) weighing max(T_j, 1) where T_j is the KV tile count of pair j's
+// q-block.  The XCD's n_x workgroups are split evenly over the G streams:
+// workgroup kx = blockIdx.x / kXcds takes stream g = kx % G and segment
+// k = kx / G of it, tiles [k C, (k + 1) C) with C = ceil(total / ns), ns =
+// n_x / G segments per stream.  So every workgroup runs at most C tiles, whatever
+// the spread of the sequence lengths, and the workgroups of segment k of
+// the streams run the same pair's tiles at about the same time, sharing its
+// K/V in the XCD's L2.  A unit cut by segment boundaries runs as pieces;
+// the last of them to finish (merge_take_last, or the one whose count
+// completes the unit's, merge_count) merges the others' partials (fragment
+// order, store_partial_frag) with its own registers, in piece order, and
+// writes the output.  The cut points follow from the lengths alone and the
+// merge order is fixed, so results do not depend on timing.
+//
+// pp_bal_locate (wave 0): the first unit (pair index j), the segment's
+// start and end, the first unit's stream start and C, into sh[0..4].
+template <int MODE>
+__device__ void pp_bal_locate(const KArgs& a, int x, int upp, int ns, int k, int* sh) {
+  const int lane = threadIdx.x & 63;
+  const int np = a.npairs > x ? (a.npairs - x + kXcds - 1) / kXcds : 0;  // pairs of the XCD
+  const int per = (np + 63) / 64;
+  const int j0 = min(np, lane * per), j1 = min(np, j0 + per);
+  auto weight = [&](int j) -> int {
+    const Work w = decode_work<MODE>(a, x + kXcds * (j * upp), 2);
+    if (!w.valid) return 1;
+    const int kv_end = kv_end_for_block(a.mask, w.qblk * kBM, w.Lq, w.Lk, w.off);
+    const int t = (kv_end + kBN - 1) / kBN;
+    return t > 1 ? t : 1;
+  };
+  int sum = 0;
+  for (int j = j0; j < j1; ++j) sum += weight(j);
+  int incl = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d);
+    if (lane >= d) incl += y;
+  }
+  const int total = __shfl(incl, 63);
+  const int C = total > ns ? (total + ns - 1) / ns : 1;
+  const int target = k * C;
+  const int excl = incl - sum;
+  if (excl <= target && target < incl) {  // one lane, or none past the end
+    int us = excl, j = j0;
+    for (;; ++j) {
+      const int W = weight(j);
+      if (target < us + W) break;
+      us += W;
+    }
+    sh[0] = j;
+    sh[1] = target;
+    sh[2] = target + min(C, total - target);
+    sh[3] = us;
+    sh[4] = C;
+  } else if (lane == 0 && target >= total) {
+    sh[0] = 0;
+    sh[1] = 0;
+    sh[2] = 0;
+    sh[3] = 0;
+    sh[4] = C;
+  }
+}
 
 // CLAIM: the unit walk by claims (KArgs::claim, ragged/paged only), a
 // separate instantiation so that the static walk keeps its registers.
 // INLINE: a ragged launch without a plan kernel (KArgs::inline_plan): the
 // item list from build_inline_plan, and the splits merged here; a separate
 // instantiation for the same reason.
-template <int DT, int D, int MODE, bool BUF, bool CLAIM = false, bool INLINE = false>
+// BAL: the balanced walk (pp_bal_locate), paged launches without a plan
+// kernel, one split; likewise separate.
+template <int DT, int D, int MODE, bool BUF, bool CLAIM = false, bool INLINE = false,
+          bool BAL = false>
 __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   static_assert(DT != FA2_DTYPE_F32, "fp32 uses the register-staged kernel");
   static_assert(!INLINE || (MODE == FA2_LAYOUT_RAGGED && !CLAIM), "inline plans: ragged, static walk");
+  static_assert(!BAL || (MODE == FA2_LAYOUT_PAGED && !CLAIM && !INLINE), "balanced walk: paged");
   constexpr bool BF = Elt<DT>::kBF;
   constexpr int DC = D / 16;  // MFMA k-steps of S (16 head dims each)
   constexpr int DB = D / 32;  // 32-dim blocks of O^T
@@ -160,6 +233,31 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   }
   const int S = INLINE ? __builtin_amdgcn_readfirstlane(ip->splits) : launch_splits(a);
   if (split >= S) return;
+  // Balanced walk: this workgroup's stream (XCD bal_x(), head pair
+  // bal_g()) and segment (bal_k()); the segment's bounds and C stay in LDS
+  // and are read at unit boundaries only, so that no scalar register is
+  // added to the tile loop's.
+  __shared__ int bal_sh[5];
+  auto bal_x = [&]() { return static_cast<int>(blockIdx.x) % kXcds; };
+  auto bal_upp = [&]() { return (group + 1) / 2; };
+  auto bal_g = [&]() { return (static_cast<int>(blockIdx.x) / kXcds) % bal_upp(); };
+  auto bal_k = [&]() { return (static_cast<int>(blockIdx.x) / kXcds) / bal_upp(); };
+  auto bal_rd = [&](int i) { return __builtin_amdgcn_readfirstlane(bal_sh[i]); };
+  if constexpr (BAL) {
+    const int ns = ((static_cast<int>(gridDim.x) - bal_x() + kXcds - 1) / kXcds) / bal_upp();
+    if (bal_k() >= ns) return;
+    if (wave == 0) pp_bal_locate<MODE>(a, bal_x(), bal_upp(), ns, bal_k(), bal_sh);
+    __syncthreads();
+  }
+  // part slot of head h of piece s of unit v (balanced walk): segment
+  // v.us / C + s of the stream, its workgroup's first (kind 0: from the
+  // segment's start) or last (kind 1: from inside to past its end) piece
+  auto bal_slot = [&](const PPUnit& v, int s, int h, int C) -> int64_t {
+    const int kf = v.us / C;
+    const int kind = (s == 0 && v.us != kf * C) ? 1 : 0;
+    const int wg = ((kf + s) * bal_upp() + bal_g()) * kXcds + bal_x();
+    return static_cast<int64_t>((wg * 2 + kind) * 2 + h);
+  };
   const bool causal = a.mask != FA2_MASK_NONE;
   char* const stage = lds + kSlotBytes + wave * OStage<kStageDims>::kBytes;
 
@@ -219,7 +317,23 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   const int xg = blockIdx.x % kXcds;
   const int n_x = (P - xg + kXcds - 1) / kXcds;  // workgroups of the group
   // next valid unit at round >= r (uniform); false when none is left
+  PPUnit cur;
   auto next_unit = [&](int& r, PPUnit& u) -> bool {
+    if constexpr (BAL) {  // r: pair index in the stream, from the first unit's on
+      // the unit's stream start: the first unit's, or the current unit's end
+      const int us = r == bal_rd(0) ? bal_rd(3) : cur.us + cur.W;
+      const int s0 = bal_rd(1), s1 = bal_rd(2);
+      if (us >= s1) return false;
+      if (!make_unit(bal_x() + kXcds * (r * bal_upp() + bal_g()), u)) return false;
+      const int W = u.T > 1 ? u.T : 1;
+      const int b = max(us, s0), e = min(us + W, s1);
+      u.us = us;
+      u.W = W;
+      u.part = !(b == us && e == us + W);
+      u.t_begin = b - us;
+      u.T = u.T > 0 ? e - b : 0;
+      return true;
+    }
     if (dyn) {
       const int L = r * kXcds + xg;
       return L >= 0 && L < a.units && make_unit(L, u);
@@ -304,8 +418,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
   };
   constexpr int kClaimLead = 2;  // tiles between the claim and the unit's last tile
 
-  int r = dyn ? static_cast<int>(blockIdx.x) / kXcds : 0;
-  PPUnit cur;
+  int r = dyn ? static_cast<int>(blockIdx.x) / kXcds : (BAL ? bal_rd(0) : 0);
   if (!next_unit(r, cur)) return;
   int gb = 0;          // tile i of the current unit is tile gb + i of this workgroup's stream
   bool pre = false;    // the current unit's Q and first tiles were issued by the previous one
@@ -550,6 +663,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       has_next = next_unit(rn, nxt);
       // (not when this unit's rows go out as partials: the waits after the
       // prefetch count the staged output stores)
+      // (a piece of the balanced walk that writes partials waits for all of
+      // them, and one that merges waits for its loads, before its stores)
       pre_next = has_next && nxt.T > 0 && S == 1 && !a.part_out;
       // Q of the next unit: this group's last S is done
       if (pre_next) load_q(nxt);
@@ -585,15 +700,92 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       has_next = next_unit(rn, nxt);
     }
 
-    if (u.hok) {
+    // this wave's rows of the output, from v / l (staged through LDS)
+    auto store_out = [&](const f32x16 (&v)[DB], float l) {
+      const float inv = 1.f / l;  // 0/0 -> NaN for a row with no key, as the reference
+      const int nrows = max(0, min(w.Lq - wq_first, kWaveRows));
+      const __amdgpu_buffer_rsrc_t out = make_rsrc_uniform(
+          static_cast<uint16_t*>(a.o) + u.o_base + static_cast<int64_t>(wq_first) * a.o_ss,
+          static_cast<uint32_t>(nrows) * static_cast<uint32_t>(a.o_ss * 2));
+      store_o_staged_buf<DT, D, kStageDims>(v, inv, stage, out, a.o_ss, lane);
+    };
+    if (BAL && u.part) {
+      // Balanced walk, a piece of a cut unit (both groups, uniform): unless
+      // every other piece has counted already, this piece's partials go out
+      // and it counts; the last piece merges all of them, in piece order,
+      // with its own from registers, and writes the output.
+      __shared__ int bal_flag[2];
+      const float l_tot = sum_xor32(l_run);
+      const int C = bal_rd(4);
+      const int kf = u.us / C;
+      const int np = (u.us + u.W - 1) / C - kf + 1;
+      const int mine = bal_k() - kf;
+      const int unit0 = ((w.pair / kXcds) * group + w.hg) * kXcds + w.pair % kXcds;
+      if (threadIdx.x == 0)
+        *static_cast<volatile int*>(&bal_flag[0]) = merge_take_last(a, unit0, np) ? 1 : 0;
+      __syncthreads();
+      bool last = *static_cast<volatile int*>(&bal_flag[0]) != 0;
+      if (!last) {
+        if (u.hok) store_partial_frag<D>(a, bal_slot(u, mine, grp, C), wq, lane, m_run, l_tot, o);
+        merge_publish();
+        __syncthreads();
+        last = merge_count(a, unit0, np, &bal_flag[1]);
+      }
+      if (last && u.hok) {
+        // the pieces' partials are read after the count that made this piece
+        // the last, which followed every other piece's stores.  Per element
+        // the sum runs over the pieces in order; the dims go in two halves
+        // (registers: this piece's O, half an accumulator, half a piece).
+        auto piece_ml = [&](int s, float& ms, float& ls) {
+          ms = m_run;
+          ls = l_tot;
+          if (s != mine) {
+            const u32x2 ml = load_partial_frag_ml(a, bal_slot(u, s, grp, C), wq, l32);
+            const uint32_t mw = ml[0], lw = ml[1];
+            ms = __builtin_bit_cast(float, mw);
+            ls = __builtin_bit_cast(float, lw);
+          }
+        };
+        float g = -INFINITY;
+        for (int s = 0; s < np; ++s) {
+          float ms, ls;
+          piece_ml(s, ms, ls);
+          g = fmaxf(g, ms);
+        }
+        const float g_use = g == -INFINITY ? 0.f : g;
+        float lsum = 0.f;
+        for (int s = 0; s < np; ++s) {
+          float ms, ls;
+          piece_ml(s, ms, ls);
+          lsum += fast_exp2(ms - g_use) * ls;
+        }
+        constexpr int kH = DB / 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          f32x16 acc[kH];
+#pragma unroll
+          for (int dd = 0; dd < kH; ++dd) acc[dd] = (f32x16){};
+          for (int s = 0; s < np; ++s) {
+            float ms, ls;
+            piece_ml(s, ms, ls);
+            const float wgt = fast_exp2(ms - g_use);
+            const int64_t slot = bal_slot(u, s, grp, C);
+#pragma unroll
+            for (int dd = 0; dd < kH; ++dd) {
+              const f32x16 x =
+                  s == mine ? o[h * kH + dd] : load_partial_frag_o<D>(a, slot, wq, lane, h * kH + dd);
+              acc[dd] += wgt * x;
+            }
+          }
+#pragma unroll
+          for (int dd = 0; dd < kH; ++dd) o[h * kH + dd] = acc[dd];
+        }
+        store_out(o, lsum);
+      }
+    } else if (u.hok) {
       const float l_tot = sum_xor32(l_run);
       if (S == 1 && !a.part_out) {
-        const float inv = 1.f / l_tot;  // 0/0 -> NaN for a row with no key, as the reference
-        const int nrows = max(0, min(w.Lq - wq_first, kWaveRows));
-        const __amdgpu_buffer_rsrc_t out = make_rsrc_uniform(
-            static_cast<uint16_t*>(a.o) + u.o_base + static_cast<int64_t>(wq_first) * a.o_ss,
-            static_cast<uint32_t>(nrows) * static_cast<uint32_t>(a.o_ss * 2));
-        store_o_staged_buf<DT, D, kStageDims>(o, inv, stage, out, a.o_ss, lane);
+        store_out(o, l_tot);
       } else {
         // partials go to the slot the one-head-per-unit layout gives this
         // head (decode_work with heads = 1), which the combine kernel reads
