@@ -189,7 +189,10 @@ enum fa2_kernel {
  * Replaces the reference's per-call torch.empty of running_sum/max/acc
  * (attention.py:852-864).  fp32 tensors with FA2_ARITH_REFERENCE at
  * head_dim 64/128 (dense, ragged) also hold fp16 copies of q, k and v there,
- * as the reference rounds every fp32 operand to fp16.  Host-only: touches
+ * as the reference rounds every fp32 operand to fp16.  Paged calls with one
+ * q-block per sequence and more two-head units than compute units hold the
+ * partials of units their balanced walk cuts into pieces (4 * CUs * 128 *
+ * (2 + head_dim) * 4 bytes).  Host-only: touches
  * no device state except a one-time, cached query of the current device's
  * compute-unit count. */
 int fa2_fwd_workspace_size(const fa2_params* p, size_t* bytes);
@@ -205,7 +208,9 @@ int fa2_fwd(const fa2_params* p, void* stream);
  * counterpart in the reference.  `p->workspace` is ignored: the ragged/paged
  * work list and the split-KV partials live in a static device array of
  * FA2_NOALLOC_SCRATCH_BYTES that the library holds on every device it runs on
- * until the process ends.  Automatic splits (num_splits = 0) are reduced until
+ * until the process ends.  Paged calls that fa2_fwd runs with the balanced
+ * walk run whole units here (the walk's partial slots do not fit the array);
+ * automatic splits (num_splits = 0) are reduced until
  * the call fits that array, and fp32 tensors whose fp16 copies do not fit
  * run the register-staged kernel instead; a call that still does not fit, or
  * a forced num_splits that does not, returns FA2_ERR_SCRATCH before any launch.  The

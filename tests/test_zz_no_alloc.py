@@ -29,7 +29,8 @@ def _gpu():
     yield
 
 
-def call(q, k, v, kw, causal, layout, noalloc, num_splits=0, alignment="top_left"):
+def call(q, k, v, kw, causal, layout, noalloc, num_splits=0, alignment="top_left",
+         max_workgroups=0):
     """One forward call through the C ABI: fa2_fwd (workspace from torch) or
     fa2_fwd_noalloc, with the parameter block flash_attention_v2 builds."""
     from kernels import _fa2
@@ -58,7 +59,8 @@ def call(q, k, v, kw, causal, layout, noalloc, num_splits=0, alignment="top_left
                   kv_len_max=kw["k_block_table"].shape[1] * kw["kv_page_size"])
     enqueue(decode=False, layout=lay, mask=mask, num_splits=num_splits, batch=B, q_heads=Hq,
             kv_heads=Hkv, head_dim=D, q_len=M, kv_len=N, q=q, k=k, v=v, out=out,
-            q_strides=strides(q), o_strides=strides(out), noalloc=noalloc, **ex)
+            q_strides=strides(q), o_strides=strides(out), noalloc=noalloc,
+            max_workgroups=max_workgroups, **ex)
     torch.cuda.synchronize()
     return out.cpu()
 
@@ -114,6 +116,28 @@ def test_noalloc_reduces_splits_to_fit():
     assert p_ws > _fa2.NOALLOC_SCRATCH_BYTES
     out = call(q, k, v, kw, False, "dense", True)
     check_all(case, "dense", False, unpack(case, "dense", out, kw))
+
+
+def test_noalloc_paged_runs_whole_units():
+    """40 paged sequences of one q-block over 128-1800 keys, Hq16/Hkv4: 320
+    two-head units, more than the CUs, so fa2_fwd takes the balanced walk
+    (units cut into pieces, whose partial slots need ~68 MB of workspace).
+    That does not fit the scratch: fa2_fwd_noalloc runs rounds of whole units,
+    which fa2_fwd runs when the grid is capped at the CU count.  Both must
+    give the same bits, twice in a row, the second on 24 sequences."""
+    import random
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = random.Random(61)
+    for n, B in enumerate((40, 24)):
+        kv = [rng.randint(128, 1800) for _ in range(B)]
+        case = make_case(B, 16, 4, 128, "cross", torch.bfloat16, "paged", 6200 + n,
+                         q_lens=[128] * B, kv_lens=kv)
+        q, k, v, kw = pack(case, "paged", device=DEV, shuffled_pages=True, seed=n)
+        print(f"noalloc paged whole units B{B}", flush=True)
+        out = call(q, k, v, kw, True, "paged", True, alignment="bottom_right")
+        rounds = call(q, k, v, kw, True, "paged", False, alignment="bottom_right",
+                      max_workgroups=cus)
+        assert same_bits(out, rounds), B
 
 
 def _workspace_bytes(q, k):
