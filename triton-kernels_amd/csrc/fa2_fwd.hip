@@ -765,7 +765,8 @@ uint64_t next_merge_tag() {
   }
 }
 
-int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) {
+int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true,
+        bool allow_bal = true) {
   int s = packed ? validate_decode(p) : validate(p);
   if (s != FA2_OK) return s;
   if (empty_problem(p)) return FA2_OK;
@@ -774,7 +775,7 @@ int run(const fa2_params* p, void* stream, bool packed, bool allow_conv = true) 
     return FA2_ERR_ALIGNMENT;
   Plan pl{};
   s = packed ? make_plan_packed(p, &pl, p->num_splits == 0)
-             : make_plan(p, &pl, p->num_splits == 0, allow_conv);
+             : make_plan(p, &pl, p->num_splits == 0, allow_conv, allow_bal);
   if (s != FA2_OK) return s;
   if (pl.total > 0 && (!p->workspace || p->workspace_bytes < pl.total)) return FA2_ERR_WORKSPACE;
 
@@ -953,11 +954,14 @@ extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
   // one fa2_fwd runs) comes first, with fewer automatic splits until its
   // workspace fits; fp32 tensors fall back to the register-staged kernel
   // only when even one split with copies does not fit.
+  bool bal = true;  // the balanced walk, while its part slots fit
   auto fit = [&](bool allow_conv) -> int {
     c = *p;
+    bal = true;
     int r = make_plan(&c, &pl, c.num_splits == 0, allow_conv);
     if (r != FA2_OK) return r;
     if (pl.bal && pl.total > cap) {  // whole units need no part slots
+      bal = false;
       r = make_plan(&c, &pl, c.num_splits == 0, allow_conv, false);
       if (r != FA2_OK) return r;
     }
@@ -982,7 +986,7 @@ extern "C" int fa2_fwd_noalloc(const fa2_params* p, void* stream) {
   if (!ws) return FA2_ERR_HIP;
   c.workspace = ws;
   c.workspace_bytes = cap;
-  return run(&c, stream, false, conv);
+  return run(&c, stream, false, conv, bal);
 }
 
 extern "C" int fa2_decode_workspace_size(const fa2_params* p, size_t* bytes) {
