@@ -173,12 +173,12 @@ def test_balanced_walk(cid):
                 n_eq += 1
                 assert torch.equal(bal[b, h].view(torch.int16), rounds[b, h].view(torch.int16)), (b, h)
     assert n_eq > 0 and n_cut > 0
-    print("  gpu calls done; oracle on 8 sequences", flush=True)
-    # the oracle on 4 sequences with cut units and 4 without (the emulated
+    print("  gpu calls done; oracle on 4 sequences", flush=True)
+    # the oracle on 2 sequences with cut units and 2 without (the emulated
     # oracle over all 40 takes minutes)
     cut_seqs = sorted({b for b, _, _ in cut})
     whole = [b for b in range(B) if b not in cut_seqs]
-    sel = cut_seqs[:4] + whole[:4]
+    sel = cut_seqs[:2] + whole[:2]
     outs = unpack(case, "paged", bal.cpu(), kw)
     sub = dataclasses.replace(case, qs=[case.qs[b] for b in sel], ks=[case.ks[b] for b in sel],
                               vs=[case.vs[b] for b in sel], q_lens=[case.q_lens[b] for b in sel],
