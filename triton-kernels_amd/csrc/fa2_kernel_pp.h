@@ -623,10 +623,19 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa2_fwd_pp_kernel(KArgs a) {
       if (grp == 0) {
         const bool claim_now = dyn && T == 1 && wave == 0;
         if (claim_now) claim_issue();
-        if (!pre) issue_first(u, gb);
-        // K(0) (and Q) have landed: what was issued after K(0) may be in
-        // flight (K(1), V(0), and the previous unit's output stores)
-        wait_vm((T > 1 ? 2 * kI : kI) + (pre ? kStores : 0));
+        if (!pre) {
+          // K(1) and V(0) go out once K(0) and Q have landed: at a launch
+          // every workgroup fetches these at once, and the first MFMA phase
+          // needs only K(0) and Q (c5 +1.5 %, c2 and c3 unchanged)
+          ld.template issue<false>(a, w, u.t_begin * kBN, kslot(0));
+          pp_wait_vm<0>();
+          if (T > 1) ld.template issue<false>(a, w, (u.t_begin + 1) * kBN, kslot(1));
+          ld.template issue<true>(a, w, u.t_begin * kBN, vslot(0));
+        } else {
+          // K(0) and Q have landed: what was issued after K(0) may be in
+          // flight (K(1), V(0), and the previous unit's output stores)
+          wait_vm((T > 1 ? 2 * kI : kI) + kStores);
+        }
         if (claim_now) {
           pp_wait_vm<0>();
           claim_publish();
