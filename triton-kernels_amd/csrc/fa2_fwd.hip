@@ -12,6 +12,7 @@
 //   * no allocation: the caller passes the workspace.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <random>
@@ -332,6 +333,23 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv 
     }
   }
   pl->splits = splits;
+  // The two-head kernel runs one workgroup of two heads per CU.  When that
+  // grid does not cover every CU, the one-head kernel's twice as many
+  // workgroups (two per CU) finish sooner.  Measured on MI355X (the
+  // reference benchmark's B16 Hq8/Hkv2 D128 bf16 points, µs per call): at
+  // q128, 64 two-head workgroups per split, the one-head kernel is faster
+  // on 23 of 24 points (dense 3-12 %, paged 3-14 %, ragged 10-24 %; ragged
+  // full kv2048 5 % slower); at q512, 256 two-head workgroups, the two-head
+  // kernel is 6-61 % faster on dense and paged points.  (Ragged items are
+  // estimated by their lower bound; grids capped by max_workgroups keep
+  // the two-head kernel.)
+  if (pl->pp && p->max_workgroups == 0) {
+    const int64_t cus = query_device ? cu_count_current_device() : 256;
+    const int64_t items =
+        p->layout == FA2_LAYOUT_RAGGED ? std::max<int64_t>(nqb, p->batch) : pl->work_ub;
+    const int64_t wgs = cdiv(items * p->kv_heads, kXcds) * kXcds * cdiv(group, 2) * splits;
+    if (wgs < cus) pl->pp = false;
+  }
   // MHA, one split: the two-head kernel pairs q-blocks of one head (B2 H32
   // L2048 D128 bf16: causal 660 -> 713 TFLOP/s, non-causal 803 -> 882).
   // Ragged and paged only when sequences average >= 4 q-blocks: a sequence
