@@ -340,15 +340,22 @@ int make_plan(const fa2_params* p, Plan* pl, bool query_device, bool allow_conv 
   // q128, 64 two-head workgroups per split, the one-head kernel is faster
   // on 23 of 24 points (dense 3-12 %, paged 3-14 %, ragged 10-24 %; ragged
   // full kv2048 5 % slower); at q512, 256 two-head workgroups, the two-head
-  // kernel is 6-61 % faster on dense and paged points.  (Ragged items are
-  // estimated by their lower bound; grids capped by max_workgroups keep
-  // the two-head kernel.)
+  // kernel is 6-61 % faster on dense and paged points.  Ragged calls whose
+  // sequences average >= 2048 visible keys keep the two-head kernel (full
+  // q128 kv2048: 50.2 us against 52.8).  (Ragged items are estimated by
+  // their lower bound; grids capped by max_workgroups keep the two-head
+  // kernel.)
   if (pl->pp && p->max_workgroups == 0) {
     const int64_t cus = query_device ? cu_count_current_device() : 256;
-    const int64_t items =
-        p->layout == FA2_LAYOUT_RAGGED ? std::max<int64_t>(nqb, p->batch) : pl->work_ub;
+    const bool ragged = p->layout == FA2_LAYOUT_RAGGED;
+    const int64_t items = ragged ? std::max<int64_t>(nqb, p->batch) : pl->work_ub;
     const int64_t wgs = cdiv(items * p->kv_heads, kXcds) * kXcds * cdiv(group, 2) * splits;
-    if (wgs < cus) pl->pp = false;
+    int64_t keys = 0;  // ragged: average visible keys per sequence
+    if (ragged && p->batch > 0) {
+      keys = p->kv_len / p->batch;
+      if (p->mask == FA2_MASK_CAUSAL_TOP_LEFT) keys = std::min<int64_t>(keys, p->q_len / p->batch);
+    }
+    if (wgs < cus && keys < 2048) pl->pp = false;
   }
   // MHA, one split: the two-head kernel pairs q-blocks of one head (B2 H32
   // L2048 D128 bf16: causal 660 -> 713 TFLOP/s, non-causal 803 -> 882).
