@@ -23,8 +23,8 @@
 //
 // K and V tiles live in three LDS slots each (tile t in slot t % 3).  The
 // waves of group 0 issue the direct-to-LDS loads of V(i+1) and K(i+2) at
-// the start of their softmax phase V(i) (or of M(i), FA2_PP_DMA_IN_M) and
-// wait for them at the end of V(i+1), just before the barrier that precedes
+// the start of their softmax phase V(i) and wait for them at the end of
+// V(i+1), just before the barrier that precedes
 // their first use (M(i+2)); the last V tile is awaited before the final
 // PV.  No slot is refilled before both groups have read it.
 //
@@ -55,12 +55,6 @@ constexpr int kPPSlots = 3;
 // (bf16 D=128): 2 beats 0 by 2-4% on c2/c3/c5.
 #ifndef FA2_PP_PRIO
 #define FA2_PP_PRIO 2
-#endif
-// 1: group 0 issues the tile loads at the start of its MFMA phase M(i)
-// (the loads of V(i+1), K(i+2) then overlap M(i) and V(i)); 0: at the
-// start of its softmax phase V(i).
-#ifndef FA2_PP_DMA_IN_M
-#define FA2_PP_DMA_IN_M 0
 #endif
 // LDS fragment reads run this many MFMAs ahead inside the MFMA phase.
 // Measured on MI355X (bf16 D=128, alternating runs on one box): 4 beats 10
