@@ -117,6 +117,40 @@ def test_workspace_sizes():
     assert rc_ws(dense_params(batch=0)) == (0, 0)
 
 
+def c4_paged_params(**kw):
+    """c4's shape: 32 paged sequences of one 128-row q-block, Hq32/Hkv8 D128
+    bf16, bottom-right causal, page 16, pool of 9042 pages."""
+    H, KH, D, M, rows = 32, 8, 128, 128, 9042 * 16
+    p = _fa2.Fa2Params()
+    p.layout, p.dtype, p.mask, p.num_splits = (_fa2.LAYOUT_PAGED, _fa2.DTYPE_BF16,
+                                               _fa2.MASK_BOTTOM_RIGHT, 0)
+    p.batch, p.q_heads, p.kv_heads, p.head_dim, p.q_len, p.kv_len = 32, H, KH, D, M, rows
+    p.q_sb, p.q_sh, p.q_ss = H * M * D, M * D, D
+    p.k_sb, p.k_sh, p.k_ss = 0, D, KH * D
+    p.v_sb, p.v_sh, p.v_ss = 0, D, KH * D
+    p.o_sb, p.o_sh, p.o_ss = p.q_sb, p.q_sh, p.q_ss
+    p.page_size, p.kv_len_max, p.k_table_stride, p.v_table_stride = 16, 8192, 512, 512
+    p.q = p.k = p.v = p.o = p.kv_indptr = p.k_block_table = p.v_block_table = 16
+    p.softmax_scale = D ** -0.5
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_paged_balanced_walk_workspace():
+    """More two-head units (512) than CUs, one q-block per sequence: the plan
+    takes the balanced walk, whose part slots (4 per workgroup of 128 rows
+    of (m, l) and D floats) set the workspace.  A capped grid keeps rounds of
+    whole units and needs only the work list."""
+    rc, n = rc_ws(c4_paged_params())
+    assert rc == 0 and n >= 4 * 256 * 128 * (2 + 128) * 4
+    rc, n = rc_ws(c4_paged_params(max_workgroups=256))
+    assert rc == 0 and n < 1 << 20
+    # forced splits and fewer units than CUs (16 sequences: 256 units) run whole units too
+    assert rc_ws(c4_paged_params(num_splits=1))[1] < 1 << 20
+    assert rc_ws(c4_paged_params(batch=16))[1] < 1 << 20
+
+
 def test_fp32_workspace_holds_fp16_copies():
     """fp32 tensors with the reference's fp16 rounding (flash_attention_v2)
     at head_dim 64/128, dense or ragged: fp16 copies of q, k and v plus one
