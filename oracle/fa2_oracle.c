@@ -29,6 +29,9 @@
  *
  * Rows are independent, so the restatement walks one query row at a time
  * through exactly the key blocks its q-block (BLOCK_M = 64, :843) visits.
+ * Built with OpenMP (oracle/Makefile), the (sequence, q head) units run on
+ * several threads; each row's arithmetic is the same sequential code, so
+ * the results do not depend on the thread count.
  */
 #include "fa2_oracle.h"
 
@@ -142,18 +145,35 @@ int fa2o_fwd(const fa2o_args* a) {
   const int64_t D = a->head_dim, BM = a->block_m, BN = a->block_n, S = a->split_k;
   const int opr = a->operand_round, prd = a->p_round;
 
+  /* (sequence, q head) units are independent and write disjoint rows:
+   * spread over threads when built with OpenMP; each row's arithmetic is
+   * the same sequential code either way */
+  const int64_t units = a->batch * a->q_heads;
+  int err = 0;
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+  {
   float* qv = (float*)malloc(sizeof(float) * D);
   float* sc = (float*)malloc(sizeof(float) * BN);
   float* acc = (float*)malloc(sizeof(float) * S * D);
   float* mm = (float*)malloc(sizeof(float) * S);
   float* ll = (float*)malloc(sizeof(float) * S);
-  if (!qv || !sc || !acc || !mm || !ll) {
-    free(qv); free(sc); free(acc); free(mm); free(ll);
-    return 4;
+  const int ok = qv && sc && acc && mm && ll;
+  if (!ok) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+    err = 4;
   }
 
-  for (int64_t b = 0; b < a->batch; ++b) {
-    for (int64_t h = 0; h < a->q_heads; ++h) {
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic)
+#endif
+  for (int64_t u = 0; u < units; ++u) {
+    {
+      if (!ok) continue;
+      const int64_t b = u / a->q_heads, h = u % a->q_heads;
       const int64_t kvh = (a->mutation == FA2O_MUT_HEAD_MAP) ? h % a->kv_heads
                                                               : h * a->kv_heads / a->q_heads;
       seq_t s;
@@ -237,7 +257,8 @@ int fa2o_fwd(const fa2o_args* a) {
     }
   }
   free(qv); free(sc); free(acc); free(mm); free(ll);
-  return 0;
+  }
+  return err;
 }
 
 /* ---- decode_attention / speculative_decode_attention --------------------
@@ -276,17 +297,34 @@ int fa2o_decode(const fa2o_args* a, int spec) {
   const int opr = a->operand_round, prd = a->p_round;
   const int causal = a->mask != FA2O_MASK_NONE;
 
+  /* (sequence, q head) units are independent and write disjoint rows:
+   * spread over threads when built with OpenMP; each row's arithmetic is
+   * the same sequential code either way */
+  const int64_t units = a->batch * a->q_heads;
+  int err = 0;
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+  {
   float* qv = (float*)malloc(sizeof(float) * D);
   float* sc = (float*)malloc(sizeof(float) * BN);
   float* acc = (float*)malloc(sizeof(float) * S * D);
   float* mm = (float*)malloc(sizeof(float) * S);
   float* ll = (float*)malloc(sizeof(float) * S);
-  if (!qv || !sc || !acc || !mm || !ll) {
-    free(qv); free(sc); free(acc); free(mm); free(ll);
-    return 4;
+  const int ok = qv && sc && acc && mm && ll;
+  if (!ok) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+    err = 4;
   }
-  for (int64_t b = 0; b < a->batch; ++b) {
-    for (int64_t h = 0; h < a->q_heads; ++h) {
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic)
+#endif
+  for (int64_t u = 0; u < units; ++u) {
+    {
+      if (!ok) continue;
+      const int64_t b = u / a->q_heads, h = u % a->q_heads;
       const int64_t kvh = (a->mutation == FA2O_MUT_HEAD_MAP) ? h % a->kv_heads
                                                               : h * a->kv_heads / a->q_heads;
       seq_t s;
@@ -378,6 +416,7 @@ int fa2o_decode(const fa2o_args* a, int spec) {
     }
   }
   free(qv); free(sc); free(acc); free(mm); free(ll);
-  return 0;
+  }
+  return err;
 }
 
