@@ -141,3 +141,23 @@ def test_inline_plan_equals_plan_kernel(heads, causal, splits):
     planned, _ = run(case, "ragged", causal, splits, max_workgroups=1 << 20)
     assert same(inline, planned)
     check_all(case, "ragged", causal, unpack(case, "ragged", inline, kw))
+
+
+@pytest.mark.parametrize("layout", ["dense", "paged"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_kernel_choice_by_grid_fill_keeps_bits(layout, causal):
+    """B16 Hq8/Hkv2 q128 (the reference benchmark's small GQA point): the
+    two-head grid (64 workgroups) would not cover the CUs, so the call runs
+    the one-head kernel; max_workgroups = CUs keeps the two-head kernel.
+    Both kernels compute the same arithmetic, so the outputs are equal bit
+    for bit, and they pass the oracle bars."""
+    n = 16
+    case = make_case(n, 8, 2, 128, "cross", torch.bfloat16, layout, 5500 + int(causal),
+                     dense_q_range=(128, 128), dense_kv_range=(512, 512), q_lens=[128] * n,
+                     kv_lens=[512] * n)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    print(f"kernel choice {layout} causal={causal}", flush=True)
+    one, kw = run(case, layout, causal, 0)
+    two, _ = run(case, layout, causal, 0, max_workgroups=cus)
+    assert same(one, two)
+    check_all(case, layout, causal, unpack(case, layout, one, kw))
